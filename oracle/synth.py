@@ -1,0 +1,55 @@
+"""Seeded synthetic inputs and reference-style weights (test oracle only).
+
+Weights follow the reference init: Linear weights ``trunc_normal_(std=0.02)``
+with absolute bounds [-2, 2] (models/timm_helpers.py:46-98, called from
+models/layer_helpers.py:36-37), biases zero (layer_helpers.py:68), RMSNorm
+weights one (models/swin.py:263-266).  The truncated normal uses the inverse
+CDF method the reference uses (uniform on [2l-1, 2u-1] -> erfinv -> scale ->
+clamp).  Everything is drawn in fp32 from a CPU ``torch.Generator``; seeds are
+1000*k + {1: weights, 2: activations, 3: target, 4: climatology}.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict
+
+import torch
+
+from .swin_ref import BLOCK_PARAM_SHAPES
+
+
+def trunc_normal(shape, std: float, gen: torch.Generator, mean: float = 0.0,
+                 a: float = -2.0, b: float = 2.0) -> torch.Tensor:
+    def cdf(v):
+        return (1.0 + math.erf(v / math.sqrt(2.0))) / 2.0
+    lo, hi = cdf((a - mean) / std), cdf((b - mean) / std)
+    t = torch.empty(shape, dtype=torch.float32)
+    t.uniform_(2 * lo - 1, 2 * hi - 1, generator=gen)
+    t.erfinv_()
+    t.mul_(std * math.sqrt(2.0)).add_(mean)
+    return t.clamp_(min=a, max=b)
+
+
+def block_params(C: int, num_heads: int, mlp_ratio: float = 4.0, seed: int = 1,
+                 random_bias: bool = False, random_norm: bool = False) -> Dict[str, torch.Tensor]:
+    """Reference-initialised parameters of one block (vanilla key names).
+    ``random_bias`` / ``random_norm`` replace the zero biases / unit norm
+    weights with random values so that tests exercise those terms."""
+    g = torch.Generator().manual_seed(seed)
+    hd = C // num_heads
+    Hm = int(C * mlp_ratio)
+    p = {}
+    for name, shp in BLOCK_PARAM_SHAPES.items():
+        shape = shp(C, hd, Hm)
+        if name.endswith(".weight") and len(shape) == 2:
+            p[name] = trunc_normal(shape, 0.02, g)
+        elif name.endswith(".bias"):
+            p[name] = (torch.randn(shape, generator=g) * 0.1) if random_bias else torch.zeros(shape)
+        else:  # norm weights
+            p[name] = (1.0 + 0.2 * torch.randn(shape, generator=g)) if random_norm else torch.ones(shape)
+    return p
+
+
+def activations(shape, seed: int = 2) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32)
