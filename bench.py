@@ -1,0 +1,243 @@
+"""Benchmark of the MI355X Swin block forward (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c2u|c1|c4]
+
+A step is one forward pass of one SwinTransformerBlock over one batch of
+synthetic input (weights: reference trunc-normal init; activations N(0,1)),
+through the fused C-ABI call nsw_swin_block_forward.  Prints one JSON line:
+tokens/s over K timed steps (inputs resident in HBM), the roofline of the
+dominant kernel from HIP events on the launch stream, the per-kernel
+breakdown, and a CPU baseline (the fp32 oracle on the host cores, on a
+bounded sample of the same workload).  One GPU only.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "neural-scaling-weather_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "Swin-block fwd tokens/s + % MFMA/HBM roofline, p4 e1024 180x360, 1 GPU"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3     # MI355X dense fp32 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+CONFIGS = {
+    # name: (B, T, H, W, C, heads, ws, shift, dtype, description)
+    "c2": (1, 1, 180, 360, 1024, 16, (9, 18), (4, 9), "bf16",
+           "config 2: shifted SwinTransformerBlock fwd, B=1 T=1, 180x360 tokens (p4 on 720x1440), "
+           "C=1024, 16 heads (hd 64), window 9x18 (400 windows x 162), shift 4x9, mlp 4x"),
+    "c2u": (1, 1, 180, 360, 1024, 16, (9, 18), (0, 0), "bf16",
+            "config 2, unshifted twin (shift 0x0)"),
+    "c1": (1, 1, 90, 180, 192, 6, (9, 18), (4, 9), "f32",
+           "config 1: shifted block fp32, 90x180 tokens, C=192, 6 heads (hd 32), window 9x18, shift 4x9"),
+    "c4": (1, 1, 360, 720, 512, 8, (9, 18), (4, 9), "bf16",
+           "config 4 block: shifted block bf16, 360x720 tokens (p2), C=512, 8 heads (hd 64), window 9x18"),
+}
+
+
+def block_flops(B, T, H, W, C, heads, ws):
+    """Algorithmic FLOPs per block (utils/flops_utils.py:15-29 GEMM + attention
+    matmul terms, unpadded): QKV, proj, fc1, fc2, QK^T, PV."""
+    M = B * T * H * W
+    L = T * ws[0] * ws[1]
+    nWb = M // L
+    hd = C // heads
+    qkv = 2 * M * C * 3 * C
+    proj = 2 * M * C * C
+    fc1 = 2 * M * C * 4 * C
+    fc2 = 2 * M * 4 * C * C
+    att = 2 * (2 * nWb * heads * L * L * hd)
+    return {"qkv": qkv, "proj": proj, "fc1": fc1, "fc2": fc2, "attention": att}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the Swin block path has no "
+                                   "multi-GPU mode here (see DESIGN.md for how it would shard)",
+                          "n_gpus": args.gpus}), flush=True)
+        sys.exit(2)
+
+    import torch
+    import nsw
+    from nsw import _lib, ops
+
+    B, T, H, W, C, heads, ws, shift, dts, desc = CONFIGS[args.config]
+    dtype = torch.bfloat16 if dts == "bf16" else torch.float32
+    dev = torch.device("cuda:0")
+    torch.manual_seed(1001)
+    blk = nsw.Block(C, heads, (H, W), ws, T, shift_size=shift).to(device=dev, dtype=dtype).eval()
+    g = torch.Generator().manual_seed(1002)
+    x = torch.randn(B, T, H, W, C, generator=g).to(device=dev, dtype=dtype)
+    M = B * T * H * W
+
+    # ---------------------------------------------------------------- timed
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            y = blk(x)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(args.steps):
+            y = blk(x)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_step = e0.elapsed_time(e1) / args.steps
+        if not torch.isfinite(y.float()).all():
+            raise RuntimeError("non-finite block output")
+
+        # ---------------------------------------------- per-kernel breakdown
+        # the same kernels, launched one op at a time with HIP events between
+        # them on the launch stream
+        pk = blk.packed()
+        eps = blk._eps(dtype)
+        names = ["gather_norm1", "qkv", "attention", "proj_scatter", "norm2", "fc1", "fc2"]
+        times = {n: [] for n in names}
+        for it in range(args.warmup + args.steps):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+            ev[0].record(stream)
+            xw = ops.rmsnorm_roll_partition(x, pk["norm1_w"], ws, shift, eps)
+            ev[1].record(stream)
+            qkv = ops.qkv_projection(xw, pk["wqkv"], pk["bqkv"], pk["qn_w"], pk["kn_w"], heads, eps)
+            ev[2].record(stream)
+            o = ops.window_attention(qkv, heads, (C // heads) ** -0.5, geometry=(H, W, ws, shift, T))
+            ev[3].record(stream)
+            h1 = ops.proj_reverse_residual(o, pk["wproj"], pk["bproj"], x, ws, shift)
+            ev[4].record(stream)
+            hn = ops.rms_norm(h1, pk["norm2_w"], eps)
+            ev[5].record(stream)
+            u = ops.linear(hn, pk["w1"], pk["b1"], epilogue=_lib.NSW_EPI_BIAS_GELU)
+            ev[6].record(stream)
+            y2 = ops.linear(u, pk["w2"], pk["b2"], residual=h1)
+            ev[7].record(stream)
+            torch.cuda.synchronize()
+            if it >= args.warmup:
+                for i, n in enumerate(names):
+                    times[n].append(ev[i].elapsed_time(ev[i + 1]))
+        same = torch.equal(y2, y)
+
+    es = 2 if dtype == torch.bfloat16 else 4
+    A = M * C * es
+    fl = block_flops(B, T, H, W, C, heads, ws)
+    peak_f = PEAK_BF16_TFLOPS if dtype == torch.bfloat16 else PEAK_F32_TFLOPS
+    work = {  # (algorithmic units per launch, bound)
+        "gather_norm1": (2 * A, "hbm"), "qkv": (fl["qkv"], "mfma"), "attention": (4 * A, "hbm"),
+        "proj_scatter": (fl["proj"], "mfma"), "norm2": (2 * A, "hbm"), "fc1": (fl["fc1"], "mfma"),
+        "fc2": (fl["fc2"], "mfma"),
+    }
+    kern = {}
+    for n in names:
+        t = statistics.mean(times[n]) * 1e-3
+        units, bound = work[n]
+        if bound == "mfma":
+            ach = units / t / 1e12
+            kern[n] = {"ms": round(t * 1e3, 4), "bound": "mfma", "achieved": round(ach, 1), "unit": "TFLOP/s",
+                       "frac": round(ach / peak_f, 4)}
+        else:
+            ach = units / t / 1e9
+            kern[n] = {"ms": round(t * 1e3, 4), "bound": "hbm", "achieved": round(ach, 1), "unit": "GB/s",
+                       "frac": round(ach / PEAK_HBM_GBS, 4)}
+    dom = max(names, key=lambda n: kern[n]["ms"])
+    d = kern[dom]
+    traffic = None
+    tf_path = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
+    if os.path.exists(tf_path):
+        with open(tf_path) as f:
+            traffic = json.load(f).get(dom)
+    roofline = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"],
+                "peak": peak_f if d["bound"] == "mfma" else PEAK_HBM_GBS, "unit": d["unit"],
+                "frac": d["frac"], "traffic": traffic}
+
+    total_flops = sum(fl.values())
+    out = {
+        "metric": METRIC,
+        "value": round(M / (ms_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dts,
+        "data": "synthetic (N(0,1) activations, reference trunc-normal(0.02) weights)",
+        "config": {"workload": desc, "tokens": M, "block_tflop": round(total_flops / 1e12, 4),
+                   "block_tflops_achieved": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
+                   "wall_s_timed": round(wall, 4), "ops_path_equals_fused": bool(same)},
+        "roofline": roofline,
+        "kernels": kern,
+    }
+
+    # ----------------------------------------------------------- CPU baseline
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, target_s):
+    """The fp32 oracle (eager PyTorch on the host cores) on a sample of the
+    same workload: the first `nb` latitude bands of windows (every token costs
+    the same; the roll wraps inside the sample)."""
+    import torch
+    from oracle import swin_ref
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    p = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
+    nb = 1
+    g = torch.Generator().manual_seed(7)
+    times = []
+    Hs = ws[0] * nb
+    xs = torch.randn(B, T, Hs, W, C, generator=g)
+    swin_ref.block_forward(xs, p, heads, ws, shift)  # warm-up
+    t_first = None
+    while True:
+        t0 = time.perf_counter()
+        swin_ref.block_forward(xs, p, heads, ws, shift)
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        if t_first is None:
+            t_first = dt
+        if sum(times) >= target_s or len(times) >= 10:
+            break
+    med = statistics.median(times)
+    toks = B * T * Hs * W
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(toks / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"fp32 oracle block (oracle/swin_ref.py, eager torch) on {nb} latitude band "
+                      f"({Hs}x{W} tokens = {toks}, C={C}), median of {len(times)} runs "
+                      f"({med:.2f} s each); cpu: {cpu_model}"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,183 @@
+/*
+ * libnsw — MI355X (gfx950) kernels for the shifted-window Swin block forward
+ * of neural-scaling-weather, behind a plain C ABI.
+ *
+ * Conventions
+ *  - All tensors are dense, row-major, device pointers; the caller allocates
+ *    every input, output and workspace (no entry point allocates).
+ *  - `dtype` is NSW_DTYPE_F32 (fp32 storage and arithmetic, the reference's
+ *    inference precision) or NSW_DTYPE_BF16 (bf16 storage, fp32 accumulation).
+ *  - `stream` is a hipStream_t passed as void*; kernels are enqueued
+ *    asynchronously, no entry point synchronises the host.
+ *  - Return value: NSW_OK (0) or an NSW_ERR_* code; nsw_last_error() returns
+ *    the thread-local message of the last failure.
+ *  - Image layout is the reference's channels-last [B, T, H, W, C]; the
+ *    window-ordered layout is [B*nW, T*ws0*ws1, C] with window index
+ *    b*nW + i*(W/ws1) + j (models/swin_helpers.py:26-51).
+ *
+ * The reference is pure Python; the entry points below replace the library
+ * calls that its Swin block makes (file:line of the reference given for
+ * each).  There is no C ABI in the reference to bind against.
+ */
+#ifndef NSW_H_
+#define NSW_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NSW_OK 0
+#define NSW_ERR_INVALID 1     /* bad shape / argument */
+#define NSW_ERR_UNSUPPORTED 2 /* valid for the reference but not implemented here */
+#define NSW_ERR_HIP 3         /* a HIP runtime call failed */
+
+#define NSW_DTYPE_F32 0
+#define NSW_DTYPE_BF16 1
+
+/* GEMM epilogues for nsw_linear. */
+#define NSW_EPI_NONE 0          /* y = x W^T                                   */
+#define NSW_EPI_BIAS 1          /* y = x W^T + b                               */
+#define NSW_EPI_BIAS_GELU 2     /* y = gelu_erf(x W^T + b)                     */
+#define NSW_EPI_BIAS_RESIDUAL 3 /* y = x W^T + b + residual                    */
+
+const char* nsw_last_error(void);
+int nsw_version(void);
+
+/* torch.roll of [B,T,H,W,C] by (s0, s1) over dims (H, W):
+ * y[b,t,h,w] = x[b,t,(h-s0) mod H,(w-s1) mod W].
+ * Replaces RollForwardReverseRollBackward.forward
+ * (distributed/mappings.py:121-132 -> distributed/helpers.py:210-212). */
+int nsw_roll_hw(const void* x, void* y, int64_t B, int64_t T, int64_t H, int64_t W, int64_t C,
+                int64_t s0, int64_t s1, int dtype, void* stream);
+
+/* window_partition (models/swin_helpers.py:26-51):
+ * [B,T,H,W,C] -> [B*nW, T, ws0, ws1, C]. */
+int nsw_window_partition(const void* x, void* windows, int64_t B, int64_t T, int64_t H,
+                         int64_t W, int64_t C, int64_t ws0, int64_t ws1, int dtype, void* stream);
+
+/* window_reverse (models/swin_helpers.py:54-77):
+ * [B*nW, T, ws0, ws1, C] -> [B,T,H,W,C]. */
+int nsw_window_reverse(const void* windows, void* x, int64_t B, int64_t T, int64_t H,
+                       int64_t W, int64_t C, int64_t ws0, int64_t ws1, int dtype, void* stream);
+
+/* Fused roll by -shift + window_partition (models/swin_helpers.py:402-412):
+ * windows[w, t, r, c] = x[b, t, (i*ws0 + r + s0) mod H, (j*ws1 + c + s1) mod W]. */
+int nsw_roll_window_partition(const void* x, void* windows, int64_t B, int64_t T, int64_t H,
+                              int64_t W, int64_t C, int64_t ws0, int64_t ws1, int64_t s0,
+                              int64_t s1, int dtype, void* stream);
+
+/* Fused window_reverse + roll by +shift (models/swin_helpers.py:420-431):
+ * exact inverse of nsw_roll_window_partition. */
+int nsw_window_reverse_roll(const void* windows, void* x, int64_t B, int64_t T, int64_t H,
+                            int64_t W, int64_t C, int64_t ws0, int64_t ws1, int64_t s0,
+                            int64_t s1, int dtype, void* stream);
+
+/* Block._make_attention_mask (models/swin_helpers.py:322-397), one GPU,
+ * causal=False: writes the additive fp32 mask [nW, T*wa, T*wa], values
+ * {0, -100}. */
+int nsw_make_attention_mask(float* mask, int64_t H, int64_t W, int64_t ws0, int64_t ws1,
+                            int64_t s0, int64_t s1, int64_t T, void* stream);
+
+/* nn.RMSNorm over the last dim (models/layer_helpers.py:101-119):
+ * y = x * rsqrt(mean(x^2) + eps) * w, rows x C. */
+int nsw_rmsnorm(const void* x, const void* w, float eps, void* y, int64_t rows, int64_t C,
+                int dtype, void* stream);
+
+/* Fused norm1 + cyclic roll by -shift + window_partition
+ * (models/swin_helpers.py:446 + :402-412): x [B,T,H,W,C] -> xw [B*nW*T*wa, C]. */
+int nsw_rmsnorm_roll_partition(const void* x, const void* w, float eps, void* xw, int64_t B,
+                               int64_t T, int64_t H, int64_t W, int64_t C, int64_t ws0,
+                               int64_t ws1, int64_t s0, int64_t s1, int dtype, void* stream);
+
+/* F.linear + BiasLayer (+ GELU / residual) (models/layer_helpers.py:41-42,71-72,
+ * models/mlp.py:80-93): y[M,N] = epi(x[M,K] . w[N,K]^T).  bias / residual may
+ * be NULL when the epilogue does not use them.  Requires K % 64 == 0 (bf16) or
+ * K % 32 == 0 (f32), N % 4 == 0. */
+int nsw_linear(const void* x, const void* w, const void* bias, const void* residual, void* y,
+               int64_t M, int64_t N, int64_t K, int epilogue, int dtype, void* stream);
+
+/* q/k/v projections with their biases and the per-head q/k RMSNorm
+ * (models/swin_helpers.py:216-234): qkv[M, 3C] = x[M,C] . wqkv[3C,C]^T + bqkv,
+ * then columns [0,C) (q) and [C,2C) (k) are RMS-normalised per head of hd
+ * columns with weights qn_w[hd], kn_w[hd].  wqkv/bqkv are the q, k, v weights
+ * / biases stacked in that order.  Requires C % 64 == 0, hd in {16,32,64}. */
+int nsw_qkv_projection(const void* x, const void* wqkv, const void* bqkv, const void* qn_w,
+                       const void* kn_w, float eps, void* qkv, int64_t M, int64_t C,
+                       int64_t num_heads, int dtype, void* stream);
+
+/* Attention core of WindowMultiHeadAttention.forward (models/swin_helpers.py:236-249):
+ * per window and head, o = softmax(q k^T * scale + mask) v, heads merged back
+ * into o[Bw*L, C].  qkv is the [Bw*L, 3C] output of nsw_qkv_projection.
+ * Mask: if `mask` is non-NULL it is the additive fp32 [nW_mask, L, L] tensor
+ * broadcast over windows (window w uses mask[w % nW_mask]); otherwise, when
+ * (s0, s1) != (0, 0) the reference's latitude shift mask is computed from
+ * indices for the geometry (H, W, ws0, ws1, s0, T), else no mask. */
+int nsw_window_attention(const void* qkv, void* o, const float* mask, int64_t nW_mask,
+                         int64_t Bw, int64_t L, int64_t C, int64_t num_heads, float scale,
+                         int64_t H, int64_t W, int64_t ws0, int64_t ws1, int64_t s0,
+                         int64_t s1, int64_t T, int dtype, void* stream);
+
+/* proj + bias + window_reverse + roll by +shift + residual
+ * (models/swin_helpers.py:250-254, :420-431, :449):
+ * y[token(m)] = o[m] . wproj^T + bproj + skip[token(m)], y and skip [B,T,H,W,C]. */
+int nsw_proj_reverse_residual(const void* o, const void* wproj, const void* bproj,
+                              const void* skip, void* y, int64_t B, int64_t T, int64_t H,
+                              int64_t W, int64_t C, int64_t ws0, int64_t ws1, int64_t s0,
+                              int64_t s1, int dtype, void* stream);
+
+/* Whole Block.forward (models/swin_helpers.py:435-459). */
+typedef struct nsw_block_params {
+  const void* norm1_w;   /* [C]          norm1.norm.weight                      */
+  const void* wqkv;      /* [3C, C]      attn.{q,k,v}.weight stacked            */
+  const void* bqkv;      /* [3C]         attn.bias{q,k,v}.bias stacked          */
+  const void* qn_w;      /* [hd]         attn.q_norm.norm.weight                */
+  const void* kn_w;      /* [hd]         attn.k_norm.norm.weight                */
+  const void* wproj;     /* [C, C]       attn.proj.weight                       */
+  const void* bproj;     /* [C]          attn.biasproj.bias                     */
+  const void* norm2_w;   /* [C]          norm2.norm.weight                      */
+  const void* w1;        /* [Hm, C]      mlp.fc1.weight                         */
+  const void* b1;        /* [Hm]         mlp.bias1.bias                         */
+  const void* w2;        /* [C, Hm]      mlp.fc2.weight                         */
+  const void* b2;        /* [C]          mlp.bias2.bias                         */
+} nsw_block_params;
+
+typedef struct nsw_block_shape {
+  int64_t B, T, H, W, C;   /* image [B,T,H,W,C]                                 */
+  int64_t num_heads;
+  int64_t ws0, ws1;        /* window_size                                       */
+  int64_t s0, s1;          /* shift_size ((0,0) for unshifted blocks)          */
+  int64_t hidden;          /* MLP hidden features = int(C * mlp_ratio)          */
+  float eps;               /* RMSNorm eps (nn.RMSNorm eps=None: finfo(dtype).eps)*/
+  int dtype;
+} nsw_block_shape;
+
+/* Bytes of device workspace nsw_swin_block_forward needs. */
+size_t nsw_block_workspace_size(const nsw_block_shape* s);
+
+/* y = Block.forward(x); x and y [B,T,H,W,C] must not alias. */
+int nsw_swin_block_forward(const void* x, void* y, const nsw_block_params* p,
+                           const nsw_block_shape* s, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* WeightedRMSE.forward (utils/losses.py:243-266) and the textbook weighted ACC.
+ * pred/target fp32 [P, H, W] with P = B*T*Cch planes (channel = plane % Cch);
+ * w float64 [H, w_cols] with w_cols = 1 (cos-lat weights, the inference path,
+ * utils/dataloaders/era5hdf5.py:159) or w_cols = W (a full map, as the
+ * reference's tests/test_metrics.py:62-63 uses); clim fp32 [Cch] or NULL (no
+ * ACC).  Writes per-plane rmse[P] = sqrt(sum_hw w (p-t)^2 / (H*W)) and, when
+ * clim != NULL, acc[P] = sum w af ao / sqrt(sum w af^2 * sum w ao^2)
+ * (float64).  Deterministic (fixed reduction order). */
+size_t nsw_weighted_metrics_workspace_size(int64_t P, int64_t H, int64_t W);
+int nsw_weighted_metrics(const float* pred, const float* target, const double* w,
+                         int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
+                         int64_t Cch, double* rmse, double* acc, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSW_H_ */

@@ -1,0 +1,325 @@
+// Window attention core: o = softmax(q k^T * scale + mask) v per (window, head)
+// (the F.scaled_dot_product_attention call of models/swin_helpers.py:247).
+//
+// bf16 path (attn_mfma_kernel): one 256-thread workgroup per (window, head).
+// K [keys x hd] and V^T [hd x keys] of the window are staged in LDS (zero
+// padded to a multiple of 32 keys).  Each wavefront takes 16-query blocks and
+//   1. computes S^T = K Q^T with v_mfma_f32_16x16x32_bf16, so that lane l
+//      holds the logits of query l%16 for keys 16*kb + 4*(l/16) + r;
+//   2. adds the additive mask (the reference's latitude shift mask computed
+//      from indices, or a materialised mask), does the softmax in the exp2
+//      domain with two cross-lane shuffles per reduction;
+//   3. reuses the probability registers directly as the B operand of
+//      O^T = V^T P^T (the k order of a 32-key step is {4g+r, 16+4g+r} for lane
+//      group g; the V^T fragment is read from LDS in the same order), and
+//   4. writes O[q][h*hd + d] with one 8-byte store per 4 head dims.
+// Padding keys get -inf logits; no FLOPs are counted for them.
+//
+// Generic path (attn_scalar_kernel, fp32 and any head dim): one thread per
+// query, online softmax over 64-key chunks staged in LDS, fp32 throughout.
+#include "nsw_common.h"
+
+namespace nsw {
+
+enum MaskMode { MASK_NONE = 0, MASK_SHIFT = 1, MASK_TENSOR = 2 };
+
+struct AttnArgs {
+  const void* qkv;
+  void* o;
+  const float* mask;
+  int nW_mask;
+  int L, C, heads;
+  float scale;
+  int mask_mode;
+  WinGeom g;
+};
+
+// Additive mask value for (window, query, key); key/query are tokens of the
+// window's T*wa sequence.
+__device__ __forceinline__ float mask_value(const AttnArgs& a, int64_t win, int q, int k,
+                                            bool last_band) {
+  if (a.mask_mode == MASK_SHIFT) {
+    if (!last_band) return 0.f;
+    const int thr = a.g.ws0 - a.g.s0;
+    const int rq = (q % a.g.wa) / a.g.ws1, rk = (k % a.g.wa) / a.g.ws1;
+    return ((rq >= thr) != (rk >= thr)) ? -100.0f : 0.0f;
+  } else if (a.mask_mode == MASK_TENSOR) {
+    const int64_t mw = win % a.nW_mask;
+    return a.mask[(mw * a.L + q) * (int64_t)a.L + k];
+  }
+  return 0.f;
+}
+
+__device__ __forceinline__ bool window_in_last_band(const AttnArgs& a, int64_t win) {
+  if (a.mask_mode != MASK_SHIFT) return false;
+  const int wi = (int)(win % a.g.nW);
+  return wi / a.g.nwb == a.g.nhb - 1;
+}
+
+// ------------------------------------------------------------ bf16 MFMA ----
+template <int HD, int NKB>
+__global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
+  constexpr int KP = ((NKB * 16 + 31) / 32) * 32;  // padded keys (multiple of 32)
+  constexpr int KS_STRIDE = HD + 8;                // bf16 elements per K row in LDS
+  constexpr int VT_STRIDE = KP + 4;                // bf16 elements per V^T row in LDS
+  constexpr int NS = HD / 32;                      // k-steps of the QK^T product
+  constexpr int NDB = HD / 16;                     // 16-wide head-dim blocks
+  constexpr int NKS = KP / 32;                     // 32-key steps of PV
+  constexpr float LOG2E = 1.4426950408889634f;
+  __shared__ __attribute__((aligned(16))) bf16 Ks[KP * KS_STRIDE];
+  __shared__ __attribute__((aligned(16))) bf16 Vt[HD * VT_STRIDE];
+
+  const int64_t win = blockIdx.x / a.heads;
+  const int head = blockIdx.x - (int)(win * a.heads);
+  const int L = a.L, C = a.C;
+  const int64_t ld = 3 * (int64_t)C;
+  const bf16* base = (const bf16*)a.qkv + win * L * ld;
+  const int tid = threadIdx.x;
+
+  // ---- stage K and V^T (zero padded)
+  constexpr int CPR = HD / 8;  // 16-byte chunks per row
+  for (int idx = tid; idx < KP * CPR; idx += 256) {
+    const int key = idx / CPR, ch = idx - key * CPR;
+    bf16x8 kv, vv;
+    if (key < L) {
+      const bf16* rowp = base + key * ld + head * HD + ch * 8;
+      kv = *reinterpret_cast<const bf16x8*>(rowp + C);
+      vv = *reinterpret_cast<const bf16x8*>(rowp + 2 * C);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { kv[e] = (bf16)0.f; vv[e] = (bf16)0.f; }
+    }
+    *reinterpret_cast<bf16x8*>(&Ks[key * KS_STRIDE + ch * 8]) = kv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VT_STRIDE + key] = vv[e];
+  }
+  __syncthreads();
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fg = lane >> 4;
+  const bool last_band = window_in_last_band(a, win);
+  const float zscale = a.scale * LOG2E;
+  const int nqb = (L + 15) / 16;
+  const int nkb = (L + 15) / 16;
+
+  for (int qb = wave; qb < nqb; qb += 4) {
+    const int q = qb * 16 + fr;
+    const int qc = q < L ? q : L - 1;
+    bf16x8 qf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      qf[s] = *reinterpret_cast<const bf16x8*>(base + qc * ld + head * HD + 32 * s + 8 * fg);
+
+    f32x4 S[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (kb < nkb) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[(kb * 16 + fr) * KS_STRIDE + 32 * s + 8 * fg]);
+          S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], S[kb], 0, 0, 0);
+        }
+      }
+    }
+    // logits in the log2 domain, mask, running max
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb * 16 + 4 * fg + r;
+        float z = -INFINITY;
+        if (kb < nkb && key < L) {
+          z = S[kb][r] * zscale;
+          if (a.mask_mode != MASK_NONE) z += mask_value(a, win, qc, key, last_band) * LOG2E;
+        }
+        S[kb][r] = z;
+        mx = fmaxf(mx, z);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = exp2f(S[kb][r] - mx);
+        S[kb][r] = p;
+        sum += p;
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+
+    // O^T = V^T P^T
+    f32x4 O[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) O[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      if (2 * ks < nkb) {
+        bf16x8 pf;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pf[r] = (bf16)S[2 * ks][r];
+          pf[4 + r] = (2 * ks + 1 < NKB) ? (bf16)S[2 * ks + 1][r] : (bf16)0.f;
+        }
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const bf16* vrow = &Vt[(db * 16 + fr) * VT_STRIDE + 32 * ks + 4 * fg];
+          bf16x4 v0 = *reinterpret_cast<const bf16x4*>(vrow);
+          bf16x4 v1 = *reinterpret_cast<const bf16x4*>(vrow + 16);
+          bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, O[db], 0, 0, 0);
+        }
+      }
+    }
+    if (q < L) {
+      const float inv = 1.0f / sum;
+      bf16* orow = (bf16*)a.o + (win * L + q) * (int64_t)C + head * HD;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        float v[4] = {O[db][0] * inv, O[db][1] * inv, O[db][2] * inv, O[db][3] * inv};
+        store4<bf16>(orow + db * 16 + 4 * fg, v);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------- generic (fp32) ----
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void attn_scalar_kernel(AttnArgs a) {
+  constexpr int KC = 64;  // keys per LDS chunk
+  __shared__ float Kc[KC][HD];
+  __shared__ float Vc[KC][HD];
+  const int64_t win = blockIdx.x / a.heads;
+  const int head = blockIdx.x - (int)(win * a.heads);
+  const int L = a.L, C = a.C;
+  const int64_t ld = 3 * (int64_t)C;
+  const T* base = (const T*)a.qkv + win * L * ld;
+  const bool last_band = window_in_last_band(a, win);
+  const int tid = threadIdx.x;
+
+  for (int q0 = 0; q0 < L; q0 += 256) {
+    const int q = q0 + tid;
+    const bool active = q < L;
+    const int qc = active ? q : L - 1;
+    float qv[HD], acc[HD];
+#pragma unroll
+    for (int d = 0; d < HD; ++d) {
+      qv[d] = to_f32(base[qc * ld + head * HD + d]) * a.scale;
+      acc[d] = 0.f;
+    }
+    float m = -INFINITY, l = 0.f;
+    for (int k0 = 0; k0 < L; k0 += KC) {
+      __syncthreads();
+      for (int idx = tid; idx < KC * HD; idx += 256) {
+        const int kk = idx / HD, d = idx - kk * HD;
+        const int key = k0 + kk;
+        float kv = 0.f, vv = 0.f;
+        if (key < L) {
+          kv = to_f32(base[key * ld + C + head * HD + d]);
+          vv = to_f32(base[key * ld + 2 * C + head * HD + d]);
+        }
+        Kc[kk][d] = kv;
+        Vc[kk][d] = vv;
+      }
+      __syncthreads();
+      const int kn = min(KC, L - k0);
+      for (int kk = 0; kk < kn; ++kk) {
+        float s = 0.f;
+#pragma unroll
+        for (int d = 0; d < HD; ++d) s += qv[d] * Kc[kk][d];
+        if (a.mask_mode != MASK_NONE) s += mask_value(a, win, qc, k0 + kk, last_band);
+        const float mn = fmaxf(m, s);
+        const float corr = expf(m - mn);
+        const float p = expf(s - mn);
+        l = l * corr + p;
+#pragma unroll
+        for (int d = 0; d < HD; ++d) acc[d] = acc[d] * corr + p * Vc[kk][d];
+        m = mn;
+      }
+    }
+    if (active) {
+      const float inv = 1.0f / l;
+      T* orow = (T*)a.o + (win * L + q) * (int64_t)C + head * HD;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) orow[d] = from_f32<T>(acc[d] * inv);
+    }
+  }
+}
+
+template <int HD>
+static int launch_mfma(const AttnArgs& a, int64_t grid, hipStream_t st) {
+  const int nkb = (a.L + 15) / 16;
+  if (nkb <= 4) hipLaunchKernelGGL((attn_mfma_kernel<HD, 4>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else if (nkb <= 8) hipLaunchKernelGGL((attn_mfma_kernel<HD, 8>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else if (nkb <= 11) hipLaunchKernelGGL((attn_mfma_kernel<HD, 11>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else if (nkb <= 16) hipLaunchKernelGGL((attn_mfma_kernel<HD, 16>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else if (nkb <= 24) hipLaunchKernelGGL((attn_mfma_kernel<HD, 24>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else return -1;
+  return 0;
+}
+
+template <typename T>
+static int launch_scalar(const AttnArgs& a, int hd, int64_t grid, hipStream_t st) {
+  switch (hd) {
+    case 16: hipLaunchKernelGGL((attn_scalar_kernel<T, 16>), dim3((unsigned)grid), dim3(256), 0, st, a); return 0;
+    case 32: hipLaunchKernelGGL((attn_scalar_kernel<T, 32>), dim3((unsigned)grid), dim3(256), 0, st, a); return 0;
+    case 64: hipLaunchKernelGGL((attn_scalar_kernel<T, 64>), dim3((unsigned)grid), dim3(256), 0, st, a); return 0;
+    case 128: hipLaunchKernelGGL((attn_scalar_kernel<T, 128>), dim3((unsigned)grid), dim3(256), 0, st, a); return 0;
+    default: return -1;
+  }
+}
+
+int check_geom(int64_t B, int64_t T, int64_t H, int64_t W, int64_t ws0, int64_t ws1, const char* what);
+
+}  // namespace nsw
+
+using namespace nsw;
+
+extern "C" int nsw_window_attention(const void* qkv, void* o, const float* mask, int64_t nW_mask,
+                                    int64_t Bw, int64_t L, int64_t C, int64_t num_heads, float scale,
+                                    int64_t H, int64_t W, int64_t ws0, int64_t ws1, int64_t s0,
+                                    int64_t s1, int64_t T, int dtype, void* stream) {
+  const char* what = "nsw_window_attention";
+  NSW_CHECK_ARG(Bw > 0 && L > 0 && C > 0 && num_heads > 0, "%s: Bw, L, C, num_heads must be positive", what);
+  NSW_CHECK_ARG(C % num_heads == 0, "%s: C not divisible by num_heads", what);
+  NSW_CHECK_ARG(C % 8 == 0, "%s: C must be a multiple of 8", what);
+  NSW_CHECK_ARG(Bw * L < (1LL << 40) && Bw * num_heads < (1LL << 31), "%s: too large", what);
+  const int hd = (int)(C / num_heads);
+  AttnArgs a{};
+  a.qkv = qkv; a.o = o; a.mask = mask; a.nW_mask = (int)nW_mask;
+  a.L = (int)L; a.C = (int)C; a.heads = (int)num_heads; a.scale = scale;
+  if (mask) {
+    NSW_CHECK_ARG(nW_mask > 0 && Bw % nW_mask == 0, "%s: Bw=%lld not a multiple of the mask's %lld windows",
+                  what, (long long)Bw, (long long)nW_mask);
+    a.mask_mode = MASK_TENSOR;
+  } else if (s0 != 0 || s1 != 0) {
+    int rc = check_geom(1, T, H, W, ws0, ws1, what);
+    if (rc) return rc;
+    NSW_CHECK_ARG(s0 >= 0 && s0 < ws0 && s1 >= 0 && s1 < ws1, "%s: shift must lie in [0, window)", what);
+    NSW_CHECK_ARG(L == T * ws0 * ws1, "%s: L=%lld != T*ws0*ws1", what, (long long)L);
+    a.g = WinGeom::make(1, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)s0, (int)s1);
+    NSW_CHECK_ARG(Bw % a.g.nW == 0, "%s: Bw not a multiple of the image's windows", what);
+    a.mask_mode = MASK_SHIFT;
+  } else {
+    a.mask_mode = MASK_NONE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t grid = Bw * num_heads;
+  if (dtype == NSW_DTYPE_BF16) {
+    int rc = -1;
+    if (hd == 64) rc = launch_mfma<64>(a, grid, st);
+    else if (hd == 32) rc = launch_mfma<32>(a, grid, st);
+    if (rc != 0) rc = launch_scalar<bf16>(a, hd, grid, st);
+    if (rc != 0) return set_error(NSW_ERR_UNSUPPORTED, "%s: head_dim=%d, L=%lld unsupported", what, hd, (long long)L);
+  } else if (dtype == NSW_DTYPE_F32) {
+    if (launch_scalar<float>(a, hd, grid, st) != 0)
+      return set_error(NSW_ERR_UNSUPPORTED, "%s: head_dim=%d unsupported (16, 32, 64, 128)", what, hd);
+  } else {
+    return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, dtype);
+  }
+  return check_launch(what);
+}

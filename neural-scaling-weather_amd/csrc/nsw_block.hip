@@ -1,0 +1,93 @@
+// Whole Block.forward (models/swin_helpers.py:435-459) as one C-ABI call:
+//
+//   K1  xw  = rmsnorm(x; norm1) gathered to window order with the roll by -shift
+//   K2  qkv = xw . [Wq;Wk;Wv]^T + b, per-head RMSNorm of q and k   (MFMA GEMM)
+//   K3  o   = window attention(qkv) with the shift mask from indices
+//   K4  h1  = scatter_to_tokens(o . Wproj^T + bproj) + x           (MFMA GEMM)
+//   K5  hn  = rmsnorm(h1; norm2)
+//   K6  u   = gelu(hn . W1^T + b1)                                 (MFMA GEMM)
+//   K7  y   = u . W2^T + b2 + h1                                   (MFMA GEMM)
+//
+// Workspace (dtype elements): A [M*C] holds xw, then o, then hn; Q [M*max(3C,
+// Hm)] holds qkv, then u; H1 [M*C] holds h1.  M = B*T*H*W tokens.
+#include "nsw_common.h"
+
+namespace nsw {
+int gemm_qkv(const void* x, const void* wqkv, const void* bqkv, const void* qn_w, const void* kn_w,
+             float eps, void* qkv, int64_t M, int64_t C, int64_t num_heads, int dtype, void* stream);
+int gemm_proj_scatter(const void* o, const void* wproj, const void* bproj, const void* skip, void* y,
+                      int64_t B, int64_t T, int64_t H, int64_t W, int64_t C, int64_t ws0, int64_t ws1,
+                      int64_t s0, int64_t s1, int dtype, void* stream);
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct BlockLayout {
+  size_t a, q, h1, total;
+};
+
+static BlockLayout block_layout(const nsw_block_shape* s) {
+  BlockLayout l{};
+  const size_t es = dtype_size(s->dtype);
+  const size_t M = (size_t)(s->B * s->T * s->H * s->W);
+  const size_t C = (size_t)s->C;
+  const size_t wq = (size_t)(3 * s->C > s->hidden ? 3 * s->C : s->hidden);
+  l.a = 0;
+  l.q = align256(M * C * es);
+  l.h1 = l.q + align256(M * wq * es);
+  l.total = l.h1 + align256(M * C * es);
+  return l;
+}
+}  // namespace nsw
+
+using namespace nsw;
+
+extern "C" size_t nsw_block_workspace_size(const nsw_block_shape* s) {
+  if (!s || s->B <= 0 || s->T <= 0 || s->H <= 0 || s->W <= 0 || s->C <= 0 || s->hidden <= 0) return 0;
+  return block_layout(s).total;
+}
+
+extern "C" int nsw_swin_block_forward(const void* x, void* y, const nsw_block_params* p,
+                                      const nsw_block_shape* s, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  const char* what = "nsw_swin_block_forward";
+  NSW_CHECK_ARG(p && s && x && y, "%s: null argument", what);
+  NSW_CHECK_ARG(x != (const void*)y, "%s: x and y must not alias", what);
+  NSW_CHECK_ARG(s->num_heads > 0 && s->C % s->num_heads == 0, "%s: C not divisible by num_heads", what);
+  NSW_CHECK_ARG(s->hidden > 0, "%s: hidden must be positive", what);
+  const size_t need = nsw_block_workspace_size(s);
+  NSW_CHECK_ARG(workspace && workspace_bytes >= need, "%s: workspace of %zu bytes needed", what, need);
+  const BlockLayout lay = block_layout(s);
+  char* ws = (char*)workspace;
+  void* A = ws + lay.a;
+  void* Q = ws + lay.q;
+  void* H1 = ws + lay.h1;
+  const int64_t M = s->B * s->T * s->H * s->W;
+  const int64_t C = s->C;
+  const int64_t L = s->T * s->ws0 * s->ws1;
+  const int64_t hd = C / s->num_heads;
+  int rc;
+  // K1
+  rc = nsw_rmsnorm_roll_partition(x, p->norm1_w, s->eps, A, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1,
+                                  s->s0, s->s1, s->dtype, stream);
+  if (rc) return rc;
+  // K2
+  rc = gemm_qkv(A, p->wqkv, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, M, C, s->num_heads, s->dtype, stream);
+  if (rc) return rc;
+  // K3 (o overwrites xw in A)
+  rc = nsw_window_attention(Q, A, nullptr, 0, M / L, L, C, s->num_heads, 1.0f / sqrtf((float)hd), s->H,
+                            s->W, s->ws0, s->ws1, s->s0, s->s1, s->T, s->dtype, stream);
+  if (rc) return rc;
+  // K4
+  rc = gemm_proj_scatter(A, p->wproj, p->bproj, x, H1, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1, s->s0,
+                         s->s1, s->dtype, stream);
+  if (rc) return rc;
+  // K5 (hn overwrites o in A)
+  rc = nsw_rmsnorm(H1, p->norm2_w, s->eps, A, M, C, s->dtype, stream);
+  if (rc) return rc;
+  // K6 (u overwrites qkv in Q)
+  rc = nsw_linear(A, p->w1, p->b1, nullptr, Q, M, s->hidden, C, NSW_EPI_BIAS_GELU, s->dtype, stream);
+  if (rc) return rc;
+  // K7
+  rc = nsw_linear(Q, p->w2, p->b2, H1, y, M, C, s->hidden, NSW_EPI_BIAS_RESIDUAL, s->dtype, stream);
+  return rc;
+}

@@ -1,0 +1,158 @@
+// Shared device/host helpers of libnsw (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/nsw.h"
+
+namespace nsw {
+
+typedef __bf16 bf16;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+
+// ---------------------------------------------------------------- errors ----
+// Every C-ABI entry point returns NSW_OK or an error code and leaves a
+// human-readable message in a thread-local buffer (nsw_last_error()).
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+#define NSW_CHECK_ARG(cond, ...)                                  \
+  do {                                                            \
+    if (!(cond)) return ::nsw::set_error(NSW_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+inline size_t dtype_size(int dtype) { return dtype == NSW_DTYPE_BF16 ? 2 : 4; }
+
+// ------------------------------------------------------------ conversions ---
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+// v_cvt_pk_bf16_f32: round to nearest even, as torch's float -> bfloat16 cast.
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
+
+// 16-byte vector of T (8 bf16 or 4 f32), the unit of every global load/store.
+template <typename T> struct Vec16 { static constexpr int N = 16 / sizeof(T); };
+
+template <typename T>
+__device__ __forceinline__ void load16(const T* p, float* out) {
+  if constexpr (sizeof(T) == 2) {
+    bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = (float)v[i];
+  } else {
+    f32x4 v = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = v[i];
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store16(T* p, const float* in) {
+  if constexpr (sizeof(T) == 2) {
+    bf16x8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (bf16)in[i];
+    *reinterpret_cast<bf16x8*>(p) = v;
+  } else {
+    f32x4 v = {in[0], in[1], in[2], in[3]};
+    *reinterpret_cast<f32x4*>(p) = v;
+  }
+}
+
+// 4 consecutive values (8 B for bf16, 16 B for f32).
+template <typename T>
+__device__ __forceinline__ void load4(const T* p, float* out) {
+  if constexpr (sizeof(T) == 2) {
+    bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+    out[0] = (float)v[0]; out[1] = (float)v[1]; out[2] = (float)v[2]; out[3] = (float)v[3];
+  } else {
+    f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const float* in) {
+  if constexpr (sizeof(T) == 2) {
+    bf16x4 v = {(bf16)in[0], (bf16)in[1], (bf16)in[2], (bf16)in[3]};
+    *reinterpret_cast<bf16x4*>(p) = v;
+  } else {
+    f32x4 v = {in[0], in[1], in[2], in[3]};
+    *reinterpret_cast<f32x4*>(p) = v;
+  }
+}
+
+// ---------------------------------------------------------- wave helpers ----
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// ------------------------------------------------------- window geometry ----
+// Window-ordered row m of the [B*nW, T*ws0*ws1, C] matrix <-> token of the
+// [B, T, H, W, C] image, with the cyclic shift folded in:
+//   row m = ((b*nW + i*nwb + j)*T + t)*wa + r*ws1 + c
+//   token = ((b*T + t)*H + (i*ws0 + r + s0) mod H)*W + (j*ws1 + c + s1) mod W
+// (roll by -shift, window_partition; the inverse is window_reverse followed by
+//  the roll by +shift).
+struct WinGeom {
+  int B, T, H, W, ws0, ws1, s0, s1;
+  int nhb, nwb, nW, wa, L;  // bands, windows per band, windows per image, ws0*ws1, T*wa
+
+  __host__ __device__ static WinGeom make(int B, int T, int H, int W, int ws0, int ws1, int s0, int s1) {
+    WinGeom g;
+    g.B = B; g.T = T; g.H = H; g.W = W; g.ws0 = ws0; g.ws1 = ws1;
+    // normalise shifts into [0, H) / [0, W)
+    g.s0 = ((s0 % H) + H) % H;
+    g.s1 = ((s1 % W) + W) % W;
+    g.nhb = H / ws0; g.nwb = W / ws1; g.nW = g.nhb * g.nwb; g.wa = ws0 * ws1; g.L = T * g.wa;
+    return g;
+  }
+
+  __device__ __forceinline__ int64_t token_of_row(int64_t m) const {
+    int64_t win = m / L;
+    int p = (int)(m - win * L);
+    int t = p / wa;
+    int rr = p - t * wa;
+    int r = rr / ws1;
+    int c = rr - r * ws1;
+    int64_t b = win / nW;
+    int wi = (int)(win - b * nW);
+    int i = wi / nwb;
+    int j = wi - i * nwb;
+    int h = i * ws0 + r + s0; if (h >= H) h -= H;
+    int w = j * ws1 + c + s1; if (w >= W) w -= W;
+    return ((b * T + t) * H + h) * (int64_t)W + w;
+  }
+
+  __device__ __forceinline__ int64_t row_of_token(int64_t tok) const {
+    int64_t bt = tok / ((int64_t)H * W);
+    int hw = (int)(tok - bt * (int64_t)H * W);
+    int h = hw / W;
+    int w = hw - h * W;
+    int64_t b = bt / T;
+    int t = (int)(bt - b * T);
+    int hs = h - s0; if (hs < 0) hs += H;
+    int wsft = w - s1; if (wsft < 0) wsft += W;
+    int i = hs / ws0, r = hs - i * ws0;
+    int j = wsft / ws1, c = wsft - j * ws1;
+    int64_t win = b * nW + i * nwb + j;
+    return (win * T + t) * wa + r * ws1 + c;
+  }
+};
+
+}  // namespace nsw

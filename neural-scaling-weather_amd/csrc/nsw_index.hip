@@ -1,0 +1,227 @@
+// Row-permutation kernels (roll, window partition / reverse, the fused
+// norm1 + roll + partition gather) and RMSNorm, plus the shift-mask builder.
+//
+// All of them move whole C-contiguous rows: one wavefront per output row,
+// 16-byte vector loads/stores (8 bf16 or 4 f32 per lane), so every row is read
+// and written as full 64-byte-aligned segments.  HBM-bound: 2*C*sizeof(T)
+// bytes per row.
+#include "nsw_common.h"
+
+namespace nsw {
+
+enum RowMap { MAP_IDENTITY = 0, MAP_PARTITION = 1, MAP_REVERSE = 2, MAP_ROLL = 3 };
+
+// Source row of output row m for each map.
+template <int MAP>
+__device__ __forceinline__ int64_t src_row(int64_t m, const WinGeom& g) {
+  if constexpr (MAP == MAP_IDENTITY) {
+    return m;
+  } else if constexpr (MAP == MAP_PARTITION) {
+    return g.token_of_row(m);          // window-ordered row <- token (roll by -s folded in)
+  } else if constexpr (MAP == MAP_REVERSE) {
+    return g.row_of_token(m);          // token <- window-ordered row (roll by +s folded in)
+  } else {
+    // torch.roll by (s0, s1): y[h, w] = x[(h - s0) mod H, (w - s1) mod W]
+    int64_t bt = m / ((int64_t)g.H * g.W);
+    int hw = (int)(m - bt * (int64_t)g.H * g.W);
+    int h = hw / g.W, w = hw - h * g.W;
+    int hs = h - g.s0; if (hs < 0) hs += g.H;
+    int wsr = w - g.s1; if (wsr < 0) wsr += g.W;
+    return (bt * g.H + hs) * (int64_t)g.W + wsr;
+  }
+}
+
+// One wave per row; CH = number of 16-byte chunks per lane (C <= 64*CH*VEC).
+template <typename T, int MAP, bool NORM, int CH>
+__global__ __launch_bounds__(256) void row_map_kernel(const T* __restrict__ x,
+                                                      const T* __restrict__ w, float eps,
+                                                      T* __restrict__ y, int64_t rows, int C,
+                                                      WinGeom g) {
+  constexpr int VEC = Vec16<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= rows) return;
+  const int64_t s = src_row<MAP>(m, g);
+  const T* xr = x + s * C;
+  T* yr = y + m * C;
+  float v[CH][VEC];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c0 = (lane + 64 * k) * VEC;
+    if (c0 < C) {
+      load16<T>(xr + c0, v[k]);
+      if constexpr (NORM) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) ss += v[k][e] * v[k][e];
+      }
+    }
+  }
+  float rs = 1.f;
+  if constexpr (NORM) {
+    ss = wave_sum(ss);
+    rs = 1.0f / sqrtf(ss / (float)C + eps);
+  }
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c0 = (lane + 64 * k) * VEC;
+    if (c0 < C) {
+      if constexpr (NORM) {
+        float wv[VEC];
+        load16<T>(w + c0, wv);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[k][e] = (v[k][e] * rs) * wv[e];
+      }
+      store16<T>(yr + c0, v[k]);
+    }
+  }
+}
+
+template <typename T, int MAP, bool NORM>
+static int launch_row_map(const void* x, const void* w, float eps, void* y, int64_t rows,
+                          int64_t C, const WinGeom& g, hipStream_t st, const char* what) {
+  constexpr int VEC = Vec16<T>::N;
+  NSW_CHECK_ARG(C > 0 && C % VEC == 0, "%s: C=%lld must be a positive multiple of %d", what,
+                (long long)C, VEC);
+  NSW_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0 &&
+                    (!NORM || ((uintptr_t)w % 16) == 0),
+                "%s: pointers must be 16-byte aligned", what);
+  if (rows == 0) return NSW_OK;
+  const int64_t per_lane = (C / VEC + 63) / 64;
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  const T* xp = (const T*)x;
+  const T* wp = (const T*)w;
+  T* yp = (T*)y;
+  if (per_lane <= 1)
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 1>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+  else if (per_lane <= 2)
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 2>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+  else if (per_lane <= 4)
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 4>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+  else if (per_lane <= 8)
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 8>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+  else
+    return set_error(NSW_ERR_UNSUPPORTED, "%s: C=%lld too large (max %d)", what, (long long)C, 64 * 8 * VEC);
+  return check_launch(what);
+}
+
+template <int MAP, bool NORM>
+static int dispatch_row_map(int dtype, const void* x, const void* w, float eps, void* y,
+                            int64_t rows, int64_t C, const WinGeom& g, void* stream,
+                            const char* what) {
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NSW_DTYPE_BF16) return launch_row_map<bf16, MAP, NORM>(x, w, eps, y, rows, C, g, st, what);
+  if (dtype == NSW_DTYPE_F32) return launch_row_map<float, MAP, NORM>(x, w, eps, y, rows, C, g, st, what);
+  return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, dtype);
+}
+
+int check_geom(int64_t B, int64_t T, int64_t H, int64_t W, int64_t ws0, int64_t ws1, const char* what) {
+  NSW_CHECK_ARG(B > 0 && T > 0 && H > 0 && W > 0 && ws0 > 0 && ws1 > 0,
+                "%s: all of B,T,H,W,ws0,ws1 must be positive", what);
+  NSW_CHECK_ARG(H % ws0 == 0 && W % ws1 == 0, "%s: H=%lld, W=%lld not divisible by window (%lld,%lld)",
+                what, (long long)H, (long long)W, (long long)ws0, (long long)ws1);
+  NSW_CHECK_ARG(B * T * H * W < ((int64_t)1 << 40) && H * W < ((int64_t)1 << 31),
+                "%s: image too large", what);
+  return NSW_OK;
+}
+
+// Additive shift mask [nW, L, L] (closed form of Block._make_attention_mask).
+__global__ void make_mask_kernel(float* __restrict__ mask, WinGeom g, int64_t total) {
+  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int64_t LL = (int64_t)g.L * g.L;
+  const int wi = (int)(idx / LL);
+  const int pq = (int)(idx - (int64_t)wi * LL);
+  const int p = pq / g.L, q = pq - p * g.L;
+  float v = 0.f;
+  if ((g.s0 != 0 || g.s1 != 0) && wi / g.nwb == g.nhb - 1) {
+    const int rp = (p % g.wa) / g.ws1, rq = (q % g.wa) / g.ws1;
+    const int thr = g.ws0 - g.s0;
+    if ((rp >= thr) != (rq >= thr)) v = -100.0f;
+  }
+  mask[idx] = v;
+}
+
+}  // namespace nsw
+
+using namespace nsw;
+
+extern "C" int nsw_roll_hw(const void* x, void* y, int64_t B, int64_t T, int64_t H, int64_t W,
+                           int64_t C, int64_t s0, int64_t s1, int dtype, void* stream) {
+  int rc = check_geom(B, T, H, W, 1, 1, "nsw_roll_hw");
+  if (rc) return rc;
+  WinGeom g = WinGeom::make((int)B, (int)T, (int)H, (int)W, 1, 1, (int)(s0 % H), (int)(s1 % W));
+  return dispatch_row_map<MAP_ROLL, false>(dtype, x, nullptr, 0.f, y, B * T * H * W, C, g, stream, "nsw_roll_hw");
+}
+
+extern "C" int nsw_window_partition(const void* x, void* windows, int64_t B, int64_t T, int64_t H,
+                                    int64_t W, int64_t C, int64_t ws0, int64_t ws1, int dtype,
+                                    void* stream) {
+  int rc = check_geom(B, T, H, W, ws0, ws1, "nsw_window_partition");
+  if (rc) return rc;
+  WinGeom g = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, 0, 0);
+  return dispatch_row_map<MAP_PARTITION, false>(dtype, x, nullptr, 0.f, windows, B * T * H * W, C, g,
+                                                stream, "nsw_window_partition");
+}
+
+extern "C" int nsw_window_reverse(const void* windows, void* x, int64_t B, int64_t T, int64_t H,
+                                  int64_t W, int64_t C, int64_t ws0, int64_t ws1, int dtype,
+                                  void* stream) {
+  int rc = check_geom(B, T, H, W, ws0, ws1, "nsw_window_reverse");
+  if (rc) return rc;
+  WinGeom g = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, 0, 0);
+  return dispatch_row_map<MAP_REVERSE, false>(dtype, windows, nullptr, 0.f, x, B * T * H * W, C, g,
+                                              stream, "nsw_window_reverse");
+}
+
+extern "C" int nsw_roll_window_partition(const void* x, void* windows, int64_t B, int64_t T,
+                                         int64_t H, int64_t W, int64_t C, int64_t ws0, int64_t ws1,
+                                         int64_t s0, int64_t s1, int dtype, void* stream) {
+  int rc = check_geom(B, T, H, W, ws0, ws1, "nsw_roll_window_partition");
+  if (rc) return rc;
+  WinGeom g = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
+  return dispatch_row_map<MAP_PARTITION, false>(dtype, x, nullptr, 0.f, windows, B * T * H * W, C, g,
+                                                stream, "nsw_roll_window_partition");
+}
+
+extern "C" int nsw_window_reverse_roll(const void* windows, void* x, int64_t B, int64_t T, int64_t H,
+                                       int64_t W, int64_t C, int64_t ws0, int64_t ws1, int64_t s0,
+                                       int64_t s1, int dtype, void* stream) {
+  int rc = check_geom(B, T, H, W, ws0, ws1, "nsw_window_reverse_roll");
+  if (rc) return rc;
+  WinGeom g = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
+  return dispatch_row_map<MAP_REVERSE, false>(dtype, windows, nullptr, 0.f, x, B * T * H * W, C, g,
+                                              stream, "nsw_window_reverse_roll");
+}
+
+extern "C" int nsw_rmsnorm(const void* x, const void* w, float eps, void* y, int64_t rows,
+                           int64_t C, int dtype, void* stream) {
+  NSW_CHECK_ARG(rows >= 0, "nsw_rmsnorm: rows < 0");
+  WinGeom g = WinGeom::make(1, 1, 1, 1, 1, 1, 0, 0);
+  return dispatch_row_map<MAP_IDENTITY, true>(dtype, x, w, eps, y, rows, C, g, stream, "nsw_rmsnorm");
+}
+
+extern "C" int nsw_rmsnorm_roll_partition(const void* x, const void* w, float eps, void* xw,
+                                          int64_t B, int64_t T, int64_t H, int64_t W, int64_t C,
+                                          int64_t ws0, int64_t ws1, int64_t s0, int64_t s1,
+                                          int dtype, void* stream) {
+  int rc = check_geom(B, T, H, W, ws0, ws1, "nsw_rmsnorm_roll_partition");
+  if (rc) return rc;
+  WinGeom g = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
+  return dispatch_row_map<MAP_PARTITION, true>(dtype, x, w, eps, xw, B * T * H * W, C, g, stream,
+                                               "nsw_rmsnorm_roll_partition");
+}
+
+extern "C" int nsw_make_attention_mask(float* mask, int64_t H, int64_t W, int64_t ws0, int64_t ws1,
+                                       int64_t s0, int64_t s1, int64_t T, void* stream) {
+  int rc = check_geom(1, T, H, W, ws0, ws1, "nsw_make_attention_mask");
+  if (rc) return rc;
+  NSW_CHECK_ARG(s0 >= 0 && s0 < ws0 && s1 >= 0 && s1 < ws1,
+                "nsw_make_attention_mask: shift must lie in [0, window)");
+  WinGeom g = WinGeom::make(1, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)s0, (int)s1);
+  const int64_t total = (int64_t)g.nW * g.L * g.L;
+  if (total == 0) return NSW_OK;
+  hipLaunchKernelGGL(make_mask_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, mask, g, total);
+  return check_launch("nsw_make_attention_mask");
+}

@@ -1,0 +1,105 @@
+"""ctypes binding of libnsw.so (the C ABI declared in include/nsw.h).
+
+The library is loaded lazily on first use.  There is no fallback: if
+``libnsw.so`` is missing every op raises, naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnsw.so")
+
+NSW_OK = 0
+NSW_ERR_INVALID = 1
+NSW_ERR_UNSUPPORTED = 2
+NSW_ERR_HIP = 3
+
+NSW_DTYPE_F32 = 0
+NSW_DTYPE_BF16 = 1
+
+NSW_EPI_NONE = 0
+NSW_EPI_BIAS = 1
+NSW_EPI_BIAS_GELU = 2
+NSW_EPI_BIAS_RESIDUAL = 3
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_int = ctypes.c_int
+
+
+class BlockParams(ctypes.Structure):
+    _fields_ = [(n, _vp) for n in (
+        "norm1_w", "wqkv", "bqkv", "qn_w", "kn_w", "wproj", "bproj",
+        "norm2_w", "w1", "b1", "w2", "b2")]
+
+
+class BlockShape(ctypes.Structure):
+    _fields_ = [("B", _i64), ("T", _i64), ("H", _i64), ("W", _i64), ("C", _i64),
+                ("num_heads", _i64), ("ws0", _i64), ("ws1", _i64), ("s0", _i64), ("s1", _i64),
+                ("hidden", _i64), ("eps", _f32), ("dtype", _int)]
+
+
+# name -> (restype, argtypes); must match include/nsw.h
+SIGNATURES = {
+    "nsw_last_error": (ctypes.c_char_p, []),
+    "nsw_version": (_int, []),
+    "nsw_roll_hw": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+    "nsw_window_partition": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+    "nsw_window_reverse": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+    "nsw_roll_window_partition": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                         _int, _vp]),
+    "nsw_window_reverse_roll": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                       _int, _vp]),
+    "nsw_make_attention_mask": (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "nsw_rmsnorm": (_int, [_vp, _vp, _f32, _vp, _i64, _i64, _int, _vp]),
+    "nsw_rmsnorm_roll_partition": (_int, [_vp, _vp, _f32, _vp, _i64, _i64, _i64, _i64, _i64,
+                                          _i64, _i64, _i64, _i64, _int, _vp]),
+    "nsw_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
+    "nsw_qkv_projection": (_int, [_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _i64, _i64, _int, _vp]),
+    "nsw_window_attention": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _i64, _i64,
+                                    _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+    "nsw_proj_reverse_residual": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                         _i64, _i64, _i64, _i64, _int, _vp]),
+    "nsw_block_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(BlockShape)]),
+    "nsw_swin_block_forward": (_int, [_vp, _vp, ctypes.POINTER(BlockParams), ctypes.POINTER(BlockShape),
+                                      _vp, ctypes.c_size_t, _vp]),
+    "nsw_weighted_metrics_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64]),
+    "nsw_weighted_metrics": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
+                                    ctypes.c_size_t, _vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class NswError(RuntimeError):
+    """A libnsw entry point returned an error code."""
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise NswError(
+                        f"{LIB_PATH} is not built; run `python neural-scaling-weather_amd/build.py` "
+                        "(the Swin block has no non-HIP implementation)")
+                h = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(h, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = h
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != NSW_OK:
+        msg = lib().nsw_last_error().decode(errors="replace")
+        if rc == NSW_ERR_INVALID:
+            raise ValueError(f"libnsw{(' ' + what) if what else ''}: {msg}")
+        raise NswError(f"libnsw{(' ' + what) if what else ''} (code {rc}): {msg}")

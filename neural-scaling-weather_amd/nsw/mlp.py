@@ -1,0 +1,48 @@
+"""``MLP`` (models/mlp.py:14-95): fc1 -> +bias1 -> GELU(erf) -> fc2 -> +bias2.
+
+Two libnsw GEMM launches: fc1 with the bias + exact-erf GELU epilogue, fc2
+with the bias epilogue.  Dropout is the identity in eval (p = 0 in every
+config); a training-mode dropout with p > 0 is not implemented and raises.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import _lib, ops
+from .layer_helpers import BiasLayer, LinearLayer
+
+
+class MLP(nn.Module):
+    def __init__(self, in_features, hidden_features=None, out_features=None, act_layer=nn.GELU, drop=0.0):
+        super().__init__()
+        out_features = out_features or in_features
+        hidden_features = hidden_features or in_features
+        self.fc1 = LinearLayer(in_features, hidden_features,
+                               comm_metadata={"sharded": ["tp", None], "shared": ["sp1-sp2"], "reduce": ["sp1-sp2"]})
+        self.bias1 = BiasLayer(hidden_features,
+                               comm_metadata={"sharded": ["tp"], "shared": ["sp1-sp2"], "reduce": ["sp1-sp2"]})
+        self.act = act_layer()
+        self.fc2 = LinearLayer(hidden_features, out_features,
+                               comm_metadata={"sharded": [None, "tp"], "shared": ["sp1-sp2"], "reduce": ["sp1-sp2"]})
+        self.bias2 = BiasLayer(out_features,
+                               comm_metadata={"sharded": [], "shared": ["tp-sp1-sp2"], "reduce": ["sp1-sp2"]})
+        self.drop = nn.Dropout(drop)
+
+    def _check_fusable(self):
+        if not (isinstance(self.act, nn.GELU) and self.act.approximate == "none"):
+            raise NotImplementedError("libnsw fuses the exact-erf nn.GELU only")
+        if self.training and self.drop.p > 0:
+            raise NotImplementedError("dropout with p > 0 in training mode is not implemented")
+
+    def forward(self, x, residual=None):
+        """``residual`` (same shape as the output) is added in fc2's epilogue;
+        the reference adds the block's skip right after the MLP
+        (models/swin_helpers.py:456)."""
+        self._check_fusable()
+        x = x.contiguous()
+        h = ops.linear(x, self.fc1.weight, self.bias1.bias, epilogue=_lib.NSW_EPI_BIAS_GELU)
+        if residual is None:
+            return ops.linear(h, self.fc2.weight, self.bias2.bias, epilogue=_lib.NSW_EPI_BIAS)
+        return ops.linear(h, self.fc2.weight, self.bias2.bias, residual=residual.contiguous(),
+                          epilogue=_lib.NSW_EPI_BIAS_RESIDUAL)

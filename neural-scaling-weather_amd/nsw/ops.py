@@ -1,0 +1,329 @@
+"""Tensor-level wrappers of the libnsw C ABI.
+
+Every op takes / returns torch tensors on the GPU, enqueues HIP kernels on
+torch's current stream and allocates its outputs with torch (plumbing only:
+all arithmetic runs in libnsw's kernels).  Inputs must be contiguous,
+16-byte aligned, fp32 or bf16, on a HIP device; anything else raises.
+"""
+from __future__ import annotations
+
+import threading
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+_DTYPES = {torch.float32: _lib.NSW_DTYPE_F32, torch.bfloat16: _lib.NSW_DTYPE_BF16}
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"libnsw supports float32 and bfloat16 tensors, got {t.dtype}") from None
+
+
+def _dev(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("libnsw ops run on the GPU only; got a tensor on " + str(t.device))
+        if not t.is_contiguous():
+            raise RuntimeError("libnsw ops need contiguous tensors")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError("libnsw op arguments are on different devices")
+    return dev
+
+
+def _same_dtype(ref: torch.Tensor, *ts: Optional[torch.Tensor]) -> None:
+    for t in ts:
+        if t is not None and t.dtype != ref.dtype:
+            raise TypeError(f"dtype mismatch: {t.dtype} vs {ref.dtype}")
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def default_eps(dtype: torch.dtype) -> float:
+    """nn.RMSNorm(eps=None) uses finfo(input dtype).eps."""
+    return float(torch.finfo(dtype).eps)
+
+
+# ------------------------------------------------------------------ index ---
+
+def roll_hw(x: torch.Tensor, shifts: Tuple[int, int]) -> torch.Tensor:
+    """torch.roll(x, shifts, dims=(-3, -2)) of a [B,T,H,W,C] tensor."""
+    B, T, H, W, C = x.shape
+    dev = _dev(x)
+    y = torch.empty_like(x)
+    check(lib().nsw_roll_hw(x.data_ptr(), y.data_ptr(), B, T, H, W, C, int(shifts[0]), int(shifts[1]),
+                            dtype_code(x), _stream(dev)), "roll_hw")
+    return y
+
+
+def window_partition(x: torch.Tensor, window_size: Tuple[int, int]) -> torch.Tensor:
+    B, T, H, W, C = x.shape
+    ws0, ws1 = window_size
+    if H % ws0 or W % ws1:
+        raise ValueError(f"image {H}x{W} is not divisible by window {window_size}")
+    dev = _dev(x)
+    out = torch.empty((B * (H // ws0) * (W // ws1), T, ws0, ws1, C), dtype=x.dtype, device=dev)
+    check(lib().nsw_window_partition(x.data_ptr(), out.data_ptr(), B, T, H, W, C, ws0, ws1,
+                                     dtype_code(x), _stream(dev)), "window_partition")
+    return out
+
+
+def window_reverse(windows: torch.Tensor, window_size: Tuple[int, int],
+                   img_size: Tuple[int, int]) -> torch.Tensor:
+    H, W = img_size
+    ws0, ws1 = window_size
+    T, C = windows.shape[1], windows.shape[-1]
+    nw = (H // ws0) * (W // ws1)
+    if windows.shape[0] % nw:
+        raise ValueError("number of windows is not a multiple of the image's windows")
+    B = windows.shape[0] // nw
+    dev = _dev(windows)
+    out = torch.empty((B, T, H, W, C), dtype=windows.dtype, device=dev)
+    check(lib().nsw_window_reverse(windows.data_ptr(), out.data_ptr(), B, T, H, W, C, ws0, ws1,
+                                   dtype_code(windows), _stream(dev)), "window_reverse")
+    return out
+
+
+def roll_window_partition(x: torch.Tensor, window_size, shift_size) -> torch.Tensor:
+    """window_partition(torch.roll(x, -shift, (H, W)), window_size) in one pass."""
+    B, T, H, W, C = x.shape
+    ws0, ws1 = window_size
+    dev = _dev(x)
+    out = torch.empty((B * (H // ws0) * (W // ws1), T, ws0, ws1, C), dtype=x.dtype, device=dev)
+    check(lib().nsw_roll_window_partition(x.data_ptr(), out.data_ptr(), B, T, H, W, C, ws0, ws1,
+                                          int(shift_size[0]), int(shift_size[1]), dtype_code(x),
+                                          _stream(dev)), "roll_window_partition")
+    return out
+
+
+def window_reverse_roll(windows: torch.Tensor, window_size, img_size, shift_size) -> torch.Tensor:
+    """torch.roll(window_reverse(windows), +shift, (H, W)) in one pass."""
+    H, W = img_size
+    ws0, ws1 = window_size
+    T, C = windows.shape[1], windows.shape[-1]
+    B = windows.shape[0] // ((H // ws0) * (W // ws1))
+    dev = _dev(windows)
+    out = torch.empty((B, T, H, W, C), dtype=windows.dtype, device=dev)
+    check(lib().nsw_window_reverse_roll(windows.data_ptr(), out.data_ptr(), B, T, H, W, C, ws0, ws1,
+                                        int(shift_size[0]), int(shift_size[1]), dtype_code(windows),
+                                        _stream(dev)), "window_reverse_roll")
+    return out
+
+
+def make_attention_mask(H: int, W: int, window_size: Tuple[int, int], shift_size: Tuple[int, int],
+                        T: int, device) -> torch.Tensor:
+    ws0, ws1 = window_size
+    nW = (H // ws0) * (W // ws1)
+    L = T * ws0 * ws1
+    m = torch.empty((nW, L, L), dtype=torch.float32, device=device)
+    check(lib().nsw_make_attention_mask(m.data_ptr(), H, W, ws0, ws1, int(shift_size[0]),
+                                        int(shift_size[1]), T, _stream(m.device)), "make_attention_mask")
+    return m
+
+
+# ------------------------------------------------------------------- norms ---
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: Optional[float] = None) -> torch.Tensor:
+    dev = _dev(x, weight)
+    _same_dtype(x, weight)
+    C = x.shape[-1]
+    if weight.numel() != C:
+        raise ValueError(f"norm weight has {weight.numel()} elements, input has {C} features")
+    eps = default_eps(x.dtype) if eps is None else float(eps)
+    y = torch.empty_like(x)
+    check(lib().nsw_rmsnorm(x.data_ptr(), weight.data_ptr(), eps, y.data_ptr(), x.numel() // C, C,
+                            dtype_code(x), _stream(dev)), "rms_norm")
+    return y
+
+
+def rmsnorm_roll_partition(x: torch.Tensor, weight: torch.Tensor, window_size, shift_size,
+                           eps: Optional[float] = None) -> torch.Tensor:
+    """norm1 + roll by -shift + window_partition, as [B*nW, T*wa, C]."""
+    B, T, H, W, C = x.shape
+    dev = _dev(x, weight)
+    _same_dtype(x, weight)
+    eps = default_eps(x.dtype) if eps is None else float(eps)
+    ws0, ws1 = window_size
+    out = torch.empty((B * (H // ws0) * (W // ws1), T * ws0 * ws1, C), dtype=x.dtype, device=dev)
+    check(lib().nsw_rmsnorm_roll_partition(x.data_ptr(), weight.data_ptr(), eps, out.data_ptr(), B, T, H, W,
+                                           C, ws0, ws1, int(shift_size[0]), int(shift_size[1]),
+                                           dtype_code(x), _stream(dev)), "rmsnorm_roll_partition")
+    return out
+
+
+# -------------------------------------------------------------------- GEMM ---
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+           residual: Optional[torch.Tensor] = None, epilogue: Optional[int] = None) -> torch.Tensor:
+    """y = epi(x . weight^T): F.linear with an optional fused bias / GELU / residual."""
+    dev = _dev(x, weight, bias, residual)
+    _same_dtype(x, weight, bias, residual)
+    K = x.shape[-1]
+    N, Kw = weight.shape
+    if Kw != K:
+        raise ValueError(f"linear: x has {K} features, weight expects {Kw}")
+    M = x.numel() // K
+    if epilogue is None:
+        epilogue = _lib.NSW_EPI_NONE if bias is None else (
+            _lib.NSW_EPI_BIAS if residual is None else _lib.NSW_EPI_BIAS_RESIDUAL)
+    y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=dev)
+    if residual is not None and residual.shape != y.shape:
+        raise ValueError(f"residual shape {tuple(residual.shape)} != output {tuple(y.shape)}")
+    check(lib().nsw_linear(x.data_ptr(), weight.data_ptr(), _p(bias), _p(residual), y.data_ptr(), M, N, K,
+                           int(epilogue), dtype_code(x), _stream(dev)), "linear")
+    return y
+
+
+def qkv_projection(x: torch.Tensor, wqkv: torch.Tensor, bqkv: torch.Tensor, qn_w: torch.Tensor,
+                   kn_w: torch.Tensor, num_heads: int, eps: Optional[float] = None) -> torch.Tensor:
+    """[.., C] -> [.., 3C]: q|k|v = x W^T + b with per-head RMSNorm on q and k."""
+    dev = _dev(x, wqkv, bqkv, qn_w, kn_w)
+    _same_dtype(x, wqkv, bqkv, qn_w, kn_w)
+    C = x.shape[-1]
+    M = x.numel() // C
+    eps = default_eps(x.dtype) if eps is None else float(eps)
+    y = torch.empty(x.shape[:-1] + (3 * C,), dtype=x.dtype, device=dev)
+    check(lib().nsw_qkv_projection(x.data_ptr(), wqkv.data_ptr(), bqkv.data_ptr(), qn_w.data_ptr(),
+                                   kn_w.data_ptr(), eps, y.data_ptr(), M, C, num_heads, dtype_code(x),
+                                   _stream(dev)), "qkv_projection")
+    return y
+
+
+# --------------------------------------------------------------- attention ---
+
+def window_attention(qkv: torch.Tensor, num_heads: int, scale: float, mask: Optional[torch.Tensor] = None,
+                     geometry: Optional[Tuple[int, int, Tuple[int, int], Tuple[int, int], int]] = None
+                     ) -> torch.Tensor:
+    """qkv [Bw, L, 3C] -> o [Bw, L, C].  ``mask``: additive fp32 [nW, L, L] or
+    None; ``geometry`` = (H, W, window_size, shift_size, T) computes the
+    reference's shift mask from indices instead (ignored when mask is given)."""
+    Bw, L, C3 = qkv.shape
+    C = C3 // 3
+    dev = _dev(qkv, mask)
+    if mask is not None:
+        if mask.dtype != torch.float32:
+            mask = mask.float().contiguous()
+        if mask.shape[-2:] != (L, L):
+            raise ValueError(f"mask shape {tuple(mask.shape)} does not match L={L}")
+        nWm = mask.shape[0]
+    else:
+        nWm = 0
+    H = W = ws0 = ws1 = 1
+    s0 = s1 = 0
+    T = 1
+    if geometry is not None and mask is None:
+        H, W, (ws0, ws1), (s0, s1), T = geometry
+    o = torch.empty((Bw, L, C), dtype=qkv.dtype, device=dev)
+    check(lib().nsw_window_attention(qkv.data_ptr(), o.data_ptr(), _p(mask), nWm, Bw, L, C, num_heads,
+                                     float(scale), H, W, ws0, ws1, s0, s1, T, dtype_code(qkv),
+                                     _stream(dev)), "window_attention")
+    return o
+
+
+def proj_reverse_residual(o: torch.Tensor, wproj: torch.Tensor, bproj: torch.Tensor, skip: torch.Tensor,
+                          window_size, shift_size) -> torch.Tensor:
+    """skip + roll(window_reverse(o W^T + b), +shift) with skip [B,T,H,W,C]."""
+    B, T, H, W, C = skip.shape
+    dev = _dev(o, wproj, bproj, skip)
+    _same_dtype(o, wproj, bproj, skip)
+    y = torch.empty_like(skip)
+    check(lib().nsw_proj_reverse_residual(o.data_ptr(), wproj.data_ptr(), bproj.data_ptr(), skip.data_ptr(),
+                                          y.data_ptr(), B, T, H, W, C, window_size[0], window_size[1],
+                                          int(shift_size[0]), int(shift_size[1]), dtype_code(o),
+                                          _stream(dev)), "proj_reverse_residual")
+    return y
+
+
+# ------------------------------------------------------------------- block ---
+
+_ws_lock = threading.Lock()
+_workspaces = {}
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Grow-only scratch buffer per (device, stream), reused by every block
+    launched on that stream (kernels on one stream run in order)."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    with _ws_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+            _workspaces[key] = buf
+        return buf
+
+
+def block_shape(x: torch.Tensor, num_heads: int, window_size, shift_size, hidden: int,
+                eps: Optional[float]) -> _lib.BlockShape:
+    B, T, H, W, C = x.shape
+    eps = default_eps(x.dtype) if eps is None else float(eps)
+    return _lib.BlockShape(B, T, H, W, C, num_heads, window_size[0], window_size[1],
+                           int(shift_size[0]), int(shift_size[1]), hidden, eps, dtype_code(x))
+
+
+def swin_block_forward(x: torch.Tensor, packed: dict, num_heads: int, window_size, shift_size,
+                       eps: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Whole Block.forward through one C-ABI call.  ``packed`` holds the
+    tensors named like the fields of nsw_block_params."""
+    dev = _dev(x, *packed.values())
+    _same_dtype(x, *packed.values())
+    hidden = packed["w1"].shape[0]
+    shp = block_shape(x, num_heads, window_size, shift_size, hidden, eps)
+    params = _lib.BlockParams(*[packed[n].data_ptr() for n, _ in _lib.BlockParams._fields_])
+    nbytes = lib().nsw_block_workspace_size(shp)
+    ws = workspace(nbytes, dev)
+    y = torch.empty_like(x) if out is None else out
+    check(lib().nsw_swin_block_forward(x.data_ptr(), y.data_ptr(), params, shp, ws.data_ptr(), ws.numel(),
+                                       _stream(dev)), "swin_block_forward")
+    return y
+
+
+# ----------------------------------------------------------------- metrics ---
+
+def weighted_metrics(pred: torch.Tensor, target: torch.Tensor, weights: torch.Tensor,
+                     clim: Optional[torch.Tensor] = None):
+    """Per-(b,t,c) weighted RMSE and (if clim is given) ACC, float64 [B,T,C].
+    ``weights``: [H], [H, 1] (cos-lat) or [H, W] (a full map)."""
+    if pred.shape != target.shape or pred.dim() != 5:
+        raise ValueError("pred and target must be [B, T, C, H, W] of the same shape")
+    if pred.dtype != torch.float32 or target.dtype != torch.float32:
+        raise TypeError("weighted metrics take float32 fields")
+    B, T, C, H, W = pred.shape
+    dev = _dev(pred, target, clim)
+    w = weights.to(device=dev, dtype=torch.float64).contiguous()
+    if w.numel() == H:
+        w_cols = 1
+    elif w.numel() == H * W and (w.dim() < 2 or tuple(w.shape[-2:]) == (H, W)):
+        w_cols = W
+    else:
+        raise ValueError(f"weights of shape {tuple(weights.shape)} do not match a {H}x{W} field")
+    if clim is not None:
+        clim = clim.reshape(-1).to(torch.float32).contiguous()
+        if clim.numel() != C:
+            raise ValueError("climatology must have one value per channel")
+    P = B * T * C
+    rmse = torch.empty(P, dtype=torch.float64, device=dev)
+    acc = torch.empty(P, dtype=torch.float64, device=dev) if clim is not None else None
+    nbytes = lib().nsw_weighted_metrics_workspace_size(P, H, W)
+    ws = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)
+    check(lib().nsw_weighted_metrics(pred.data_ptr(), target.data_ptr(), w.data_ptr(), w_cols, _p(clim), P,
+                                     H, W, C,
+                                     rmse.data_ptr(), _p(acc), ws.data_ptr(), ws.numel(), _stream(dev)),
+          "weighted_metrics")
+    rmse = rmse.view(B, T, C)
+    return rmse, (acc.view(B, T, C) if acc is not None else None)
