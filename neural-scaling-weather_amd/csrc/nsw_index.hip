@@ -100,8 +100,10 @@ static int launch_row_map(const void* x, const void* w, float eps, void* y, int6
     hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 4>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
   else if (per_lane <= 8)
     hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 8>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+  else if (per_lane <= 16)
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 16>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
   else
-    return set_error(NSW_ERR_UNSUPPORTED, "%s: C=%lld too large (max %d)", what, (long long)C, 64 * 8 * VEC);
+    return set_error(NSW_ERR_UNSUPPORTED, "%s: C=%lld too large (max %d)", what, (long long)C, 64 * 16 * VEC);
   return check_launch(what);
 }
 
