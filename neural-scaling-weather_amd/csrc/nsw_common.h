@@ -102,6 +102,42 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Reductions over the four 16-lane rows of a wavefront (lanes l, l^16, l^32,
+// l^48), the lanes that hold one row / query in an MFMA 16x16 result block.
+// v_permlane16_swap(x, x) returns {x of even row, x of odd row} of each row
+// pair and v_permlane32_swap(x, x) {x of lower half, x of upper half}, so
+// combining the two returned values gives the xor-16 / xor-32 partner result
+// in the same operand order on every lane (pure VALU, no LDS traffic).
+//
+// Issued through inline asm: with the same value in both operands the
+// compiler's builtin lowering (ROCm 7.2 clang) folds the two results into one
+// register and returns 2x instead of x + partner.  The s_nop covers the
+// VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+__device__ __forceinline__ float rows4_sum(float x) {
+  float a = x, b = x;
+  permlane16_swap(a, b);
+  const float s = a + b;
+  float c = s, d = s;
+  permlane32_swap(c, d);
+  return c + d;
+}
+
+__device__ __forceinline__ float rows4_max(float x) {
+  float a = x, b = x;
+  permlane16_swap(a, b);
+  const float s = fmaxf(a, b);
+  float c = s, d = s;
+  permlane32_swap(c, d);
+  return fmaxf(c, d);
+}
+
 // ------------------------------------------------------- window geometry ----
 // Window-ordered row m of the [B*nW, T*ws0*ws1, C] matrix <-> token of the
 // [B, T, H, W, C] image, with the cyclic shift folded in:

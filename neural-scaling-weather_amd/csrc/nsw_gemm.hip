@@ -1,11 +1,23 @@
 // MFMA GEMM y[M,N] = epilogue(x[M,K] . w[N,K]^T) for gfx950, with the Swin
 // block's epilogues fused in.
 //
-// Tiling (both dtypes): 256 threads = 4 wavefronts, block tile 256 (m) x 128
-// (n), k tile = 128 bytes per row (64 bf16 / 32 f32), LDS double buffered
-// (2 x 384 rows x 144 B = 108 KB; the 16-byte row pad makes the 16-lane
-// ds_read_b128 phases conflict-free).  Each wave owns a 128 (m) x 64 (n)
-// sub-tile = 8 x 4 blocks of 16x16 fp32 accumulators.
+// Workgroup tile 256 (m) x 256 (n), 4 wavefronts, each owning a 128 x 128
+// sub-tile = 8 x 8 blocks of 16x16 fp32 accumulators (256 AGPRs per lane).
+//
+// Operand staging: a ring of NSTAGE = 4 LDS stages, each holding one k tile
+// of 64 bytes per row (32 bf16 / 16 f32) for the 256 x-rows and 256 w-rows
+// (32 KB).  Global -> LDS copies use gfx950's buffer_load_dwordx4 ... lds
+// (direct to LDS, no VGPR staging): each instruction writes 1 KB = 16 rows of
+// one wave's share.  Rows are XOR-swizzled in 16-byte chunks
+// (slot = chunk ^ ((row >> 2) & 3)) so that the 16-lane phases of the
+// fragment reads (16 rows, same chunk) hit 16 distinct bank groups.
+//
+// Pipeline per k tile kt: wait for this wave's copies of tile kt+1, barrier,
+// issue the copies of tile kt+3 into the stage freed by tile kt-1, then run
+// the 64 MFMAs of tile kt from registers while the 16 fragment reads of tile
+// kt+1 are interleaved between them (register double buffering).  The
+// barrier is a bare s_barrier: __syncthreads() would add a fence that waits
+// for every outstanding copy.
 //
 // The MFMA is issued "transposed": the A operand is the weight fragment
 // (rows n) and the B operand the activation fragment (rows m), so lane l of a
@@ -30,15 +42,26 @@ enum Epi {
   EPI_BIAS = NSW_EPI_BIAS,
   EPI_BIAS_GELU = NSW_EPI_BIAS_GELU,
   EPI_BIAS_RESIDUAL = NSW_EPI_BIAS_RESIDUAL,
-  EPI_QKV_HEADNORM = 10,     // bias, then per-head RMSNorm of the q and k columns
-  EPI_SCATTER_RESIDUAL = 11  // bias, row m -> token_of_row(m), + skip[token]
+  EPI_SCATTER_RESIDUAL = 11, // bias, row m -> token_of_row(m), + skip[token]
+  EPI_QKV_HN16 = 16,         // bias, then per-head RMSNorm of the q and k
+  EPI_QKV_HN32 = 32,         // columns, for head dims 16 / 32 / 64
+  EPI_QKV_HN64 = 64
 };
 
-constexpr int BM = 256;
-constexpr int BN = 128;
-constexpr int ROWB = 128;          // k-tile bytes per row
-constexpr int LDS_STRIDE = 144;    // padded row stride in LDS (bytes)
-constexpr int STAGE_BYTES = (BM + BN) * LDS_STRIDE;
+constexpr int qkv_head_dim(int epi) {
+  return (epi == EPI_QKV_HN16 || epi == EPI_QKV_HN32 || epi == EPI_QKV_HN64) ? epi : 0;
+}
+
+constexpr int BM = 256;             // activation rows (m) per workgroup tile
+constexpr int BN = 256;             // weight rows (n) per workgroup tile
+constexpr int WTM = 128;            // wave tile (m)
+constexpr int WTN = 128;            // wave tile (n)
+constexpr int MB = WTM / 16;        // 16x16 result blocks per wave along m
+constexpr int NB = WTN / 16;        // ... along n
+constexpr int ROWB = 64;            // k-tile bytes per row
+constexpr int NSTAGE = 4;           // LDS ring depth
+constexpr int STAGE_BYTES = (BM + BN) * ROWB;          // 32 KB
+constexpr int COPIES = STAGE_BYTES / (256 * 16);       // 16-byte copies per thread per tile (8)
 
 struct EpiArgs {
   const void* bias;
@@ -46,13 +69,26 @@ struct EpiArgs {
   const void* qn_w;
   const void* kn_w;
   float eps;
-  int C;       // q/k/v width for EPI_QKV_HEADNORM
-  int hd;      // head dim for EPI_QKV_HEADNORM
+  int C;       // q/k/v width for the QKV epilogues
   WinGeom geom;  // EPI_SCATTER_RESIDUAL
 };
 
+// GELU with the exact-erf form of nn.GELU(): 0.5 v (1 + erf(v / sqrt 2)).
+// erf from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7):
+//   erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-x^2),
+//   t = 1 / (1 + p x), x >= 0, odd symmetry for x < 0.
+// 1 + erf(x) is formed without cancellation for x < 0 (it equals the tail q).
 __device__ __forceinline__ float gelu_erf(float v) {
-  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+  const float x = fabsf(v) * 0.70710678118654752440f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, x, 1.0f));
+  float poly = fmaf(1.061405429f, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  poly *= t;
+  const float q = poly * __expf(-x * x);     // 1 - erf(|x|)
+  const float one_plus_erf = v >= 0.f ? 2.0f - q : q;
+  return 0.5f * v * one_plus_erf;
 }
 
 template <typename T>
@@ -80,17 +116,55 @@ __device__ __forceinline__ int xcd_remap(int bid, int ntiles) {
   return x * q + (x < rem ? x : rem) + idx;
 }
 
+// Buffer resource over a whole tensor (raw buffer, 32-bit byte offsets).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt vmcnt(N) only (expcnt / lgkmcnt fields at their "no wait" maxima).
+#define NSW_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
+
+// One 16-row x 16-byte-chunk slab per copy instruction: wave w, copy j covers
+// stage rows (w*COPIES + j)*16 .. +15; lane i writes row +i/4, slot i%4 and
+// therefore loads global chunk (i%4) ^ ((i/16)%4).
+struct CopyPlan {
+  __amdgpu_buffer_rsrc_t rsrc;  // x for waves 0-1, w for waves 2-3 (wave-uniform)
+  uint32_t voff[COPIES];        // byte offset of this lane's chunk at k tile 0
+  int lds_row0;                 // first stage row of copy 0 for this wave
+};
+
+template <typename T>
+__device__ __forceinline__ void issue_tile(const CopyPlan& cp, char* stage, int kt) {
+#pragma unroll
+  for (int j = 0; j < COPIES; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(cp.rsrc, (lds_ptr_t)(stage + (cp.lds_row0 + j * 16) * ROWB), 16,
+                                             cp.voff[j], kt * ROWB, 0, 0);
+}
+
+// Fragment reads of one k tile: W rows (A operand) and X rows (B operand).
+__device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int fg) {
+  const int slot = fg ^ ((row >> 2) & 3);
+  return *reinterpret_cast<const u32x4*>(stage + row * ROWB + slot * 16);
+}
+
 template <typename T, int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, const T* __restrict__ Wt,
                                                    T* __restrict__ Y, int M, int N, int K,
                                                    EpiArgs ea) {
-  constexpr int VEC = 16 / sizeof(T);        // elements per 16-byte chunk
   constexpr int KT = ROWB / sizeof(T);       // elements per k tile
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE_BYTES];
+  // four separate arrays (not one) so that the compiler's wait-count
+  // tracking can tell the stages' direct-to-LDS copies apart
+  __shared__ __attribute__((aligned(1024))) char lds0[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds1[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds2[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds3[STAGE_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
   const int MT = (M + BM - 1) / BM, NT = (N + BN - 1) / BN;
@@ -98,85 +172,88 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
   const int mt = tile / NT, nt = tile - mt * NT;
   const int m0 = mt * BM, n0 = nt * BN;
 
-  // ---- global -> register staging: 8 x-chunks and 4 w-chunks per thread
-  const int lrow = tid >> 3, lchunk = tid & 7;
-  const T* xsrc[8];
-  const T* wsrc[4];
+  // ---- copy plan: waves 0-1 stage the 256 x rows, waves 2-3 the 256 w rows
+  const uint32_t rowbytes = (uint32_t)K * sizeof(T);
+  CopyPlan cp;
+  const bool xside = wave < 2;
+  cp.rsrc = xside ? make_rsrc(X, (uint32_t)M * rowbytes) : make_rsrc(Wt, (uint32_t)N * rowbytes);
+  cp.lds_row0 = wave * COPIES * 16;
+  {
+    const int chunk = (lane & 3) ^ ((lane >> 4) & 3);
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    int r = m0 + p * 32 + lrow;
-    r = r < M ? r : M - 1;
-    xsrc[p] = X + (int64_t)r * K + lchunk * VEC;
+    for (int j = 0; j < COPIES; ++j) {
+      const int srow = cp.lds_row0 + j * 16 + (lane >> 2);
+      int g = xside ? m0 + srow : n0 + srow - BM;
+      const int lim = xside ? M : N;
+      g = g < lim ? g : lim - 1;   // rows past the edge re-read the last row (never stored)
+      cp.voff[j] = (uint32_t)g * rowbytes + chunk * 16;
+    }
   }
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    int r = n0 + p * 32 + lrow;
-    r = r < N ? r : N - 1;
-    wsrc[p] = Wt + (int64_t)r * K + lchunk * VEC;
-  }
-  u32x4 xr[8], wr[4];
-#define NSW_GLOAD(kt_)                                                                   \
-  do {                                                                                   \
-    const int koff_ = (kt_) * KT;                                                        \
-    _Pragma("unroll") for (int p = 0; p < 8; ++p)                                        \
-      xr[p] = *reinterpret_cast<const u32x4*>(xsrc[p] + koff_);                          \
-    _Pragma("unroll") for (int p = 0; p < 4; ++p)                                        \
-      wr[p] = *reinterpret_cast<const u32x4*>(wsrc[p] + koff_);                          \
-  } while (0)
-#define NSW_LSTORE(stage_)                                                               \
-  do {                                                                                   \
-    char* base_ = smem + (stage_) * STAGE_BYTES;                                         \
-    _Pragma("unroll") for (int p = 0; p < 8; ++p)                                        \
-      *reinterpret_cast<u32x4*>(base_ + (p * 32 + lrow) * LDS_STRIDE + lchunk * 16) = xr[p]; \
-    _Pragma("unroll") for (int p = 0; p < 4; ++p)                                        \
-      *reinterpret_cast<u32x4*>(base_ + (BM + p * 32 + lrow) * LDS_STRIDE + lchunk * 16) = wr[p]; \
-  } while (0)
 
-  f32x4 acc[4][8];
+  f32x4 acc[NB][MB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NB; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int frow = lane & 15, fg = lane >> 4;
+  const int arow = BM + wn * WTN + frow;   // w rows of this wave (A operand)
+  const int brow = wm * WTM + frow;        // x rows of this wave (B operand)
   const int nk = K / KT;
 
-  NSW_GLOAD(0);
-  NSW_LSTORE(0);
-  __syncthreads();
+  u32x4 fa[2][NB], fb[2][MB];
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int stage = kt & 1;
-    if (kt + 1 < nk) NSW_GLOAD(kt + 1);
-    const char* base = smem + stage * STAGE_BYTES;
+  // prologue: tiles 0..2 in flight, wait for tile 0, read its fragments
+  issue_tile<T>(cp, lds0, 0);
+  if (nk > 1) issue_tile<T>(cp, lds1, 1);
+  if (nk > 2) issue_tile<T>(cp, lds2, 2);
+  if (nk > 2) NSW_WAIT_VMCNT(2 * COPIES);
+  else if (nk > 1) NSW_WAIT_VMCNT(COPIES);
+  else NSW_WAIT_VMCNT(0);
+  __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int coff = (4 * s + fg) * 16;
-      u32x4 af[4], bfr[8];
+  for (int i = 0; i < NB; ++i) fa[0][i] = lds_frag(lds0, arow + i * 16, fg);
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        af[nb] = *reinterpret_cast<const u32x4*>(base + (BM + wn * 64 + nb * 16 + frow) * LDS_STRIDE + coff);
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb)
-        bfr[mb] = *reinterpret_cast<const u32x4*>(base + (wm * 128 + mb * 16 + frow) * LDS_STRIDE + coff);
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb) mfma_chunk<T>(acc[nb][mb], af[nb], bfr[mb]);
-    }
-    if (kt + 1 < nk) NSW_LSTORE(stage ^ 1);
-    __syncthreads();
+  for (int i = 0; i < MB; ++i) fb[0][i] = lds_frag(lds0, brow + i * 16, fg);
+
+  // one k tile: U = position in the 4-stage ring (compile time), k = kt + U
+#define NSW_STEP(U, CUR, NXT, ISS)                                                             \
+  {                                                                                            \
+    const int k = kt + U;                                                                      \
+    if (k < nk) {                                                                              \
+      if (k + 1 < nk) {                                                                        \
+        if (k + 2 < nk) NSW_WAIT_VMCNT(COPIES); else NSW_WAIT_VMCNT(0);                        \
+        __builtin_amdgcn_s_barrier();                                                          \
+      }                                                                                        \
+      if (k + 3 < nk) issue_tile<T>(cp, ISS, k + 3);                                           \
+      const char* nx = (k + 1 < nk) ? NXT : CUR;                                               \
+      _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                      \
+        fb[(U + 1) & 1][mb] = lds_frag(nx, brow + mb * 16, fg);                                \
+        fa[(U + 1) & 1][mb] = lds_frag(nx, arow + mb * 16, fg);                                \
+        _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                      \
+          mfma_chunk<T>(acc[nb][mb], fa[U & 1][nb], fb[U & 1][mb]);                            \
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                                     \
+        __builtin_amdgcn_sched_group_barrier(0x008, NB * (sizeof(T) == 2 ? 1 : 4), 0);         \
+      }                                                                                        \
+    }                                                                                          \
   }
 
-#undef NSW_GLOAD
-#undef NSW_LSTORE
+  for (int kt = 0; kt < nk; kt += NSTAGE) {
+    NSW_STEP(0, lds0, lds1, lds3)
+    NSW_STEP(1, lds1, lds2, lds0)
+    NSW_STEP(2, lds2, lds3, lds1)
+    NSW_STEP(3, lds3, lds0, lds2)
+  }
+#undef NSW_STEP
 
   // ---------------------------------------------------------------- epilogue
-  const int nw0 = n0 + wn * 64;           // first column of this wave
+  // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
+  //                                          [n0 + wn*WTN + nb*16 + 4*fg + r]
+  const int nw0 = n0 + wn * WTN;           // first column of this wave
   const T* bias = (const T*)ea.bias;
-  float bv[4][4];
+  float bv[NB][4];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
+  for (int nb = 0; nb < NB; ++nb) {
     const int n = nw0 + nb * 16 + fg * 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) bv[nb][r] = 0.f;
@@ -185,60 +262,63 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
     }
   }
 
-  // per-head RMSNorm weights for this lane's columns (q or k region only)
-  bool headnorm = false;
-  float nwv[4][4];
-  if constexpr (EPI == EPI_QKV_HEADNORM) {
-    const int region = nw0 / ea.C;  // 0: q, 1: k, 2: v
-    headnorm = region < 2;
-    const T* nwp = (const T*)(region == 0 ? ea.qn_w : ea.kn_w);
+  // per-head RMSNorm (QKV epilogue): a head is HDQ/16 consecutive 16-column
+  // blocks inside one of the q / k / v regions (C % 64 == 0, HDQ | 64), so
+  // whether a head is normalised is uniform across the wave
+  constexpr int HDQ = qkv_head_dim(EPI);
+  constexpr int NBH = HDQ > 0 ? HDQ / 16 : 1;   // blocks per head
+  constexpr int NHW = NB / NBH;                 // heads per wave tile
+  bool normed[NHW];
+  float nwv[NB][4];
+  if constexpr (HDQ > 0) {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int cin = (nb * 16 + fg * 4) % ea.hd;
-      if (headnorm) load4<T>(nwp + cin, nwv[nb]);
+    for (int h = 0; h < NHW; ++h) {
+      const int c0 = nw0 + h * HDQ;
+      const int region = c0 / ea.C;  // 0: q, 1: k, 2: v
+      normed[h] = region < 2 && c0 < N;
+      const T* nwp = (const T*)(region == 0 ? ea.qn_w : ea.kn_w);
+#pragma unroll
+      for (int b = 0; b < NBH; ++b)
+        if (normed[h]) load4<T>(nwp + b * 16 + fg * 4, nwv[h * NBH + b]);
     }
   }
 
 #pragma unroll
-  for (int mb = 0; mb < 8; ++mb) {
-    const int m = m0 + wm * 128 + mb * 16 + frow;
-    float v[4][4];
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = m0 + wm * WTM + mb * 16 + frow;
+    float v[NB][4];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[nb][r] = acc[nb][mb][r] + bv[nb][r];
 
-    if constexpr (EPI == EPI_QKV_HEADNORM) {
-      // head groups of (hd/16) consecutive 16-column blocks; all lanes take
-      // part in the shuffles (the branch below is wave-uniform).
-      if (headnorm) {
-        const int nbh = ea.hd >> 4;  // 1, 2 or 4
-        float ssb[4];
+    if constexpr (HDQ > 0) {
+      // sum of squares of each head: local over its blocks, then across the
+      // four lane groups holding the same row (xor 16, xor 32)
+      float ss[NHW];
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          float s = 0.f;
+      for (int h = 0; h < NHW; ++h) {
+        float s = 0.f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) s += v[nb][r] * v[nb][r];
-          s += __shfl_xor(s, 16, 64);
-          s += __shfl_xor(s, 32, 64);
-          ssb[nb] = s;
-        }
+        for (int b = 0; b < NBH; ++b)
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          float ss = 0.f;
-          const int h0 = (nb / nbh) * nbh;
+          for (int r = 0; r < 4; ++r) s += v[h * NBH + b][r] * v[h * NBH + b][r];
+        ss[h] = rows4_sum(s);
+      }
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (q >= h0 && q < h0 + nbh) ss += ssb[q];
-          const float rs = 1.0f / sqrtf(ss / (float)ea.hd + ea.eps);
+      for (int h = 0; h < NHW; ++h) {
+        if (normed[h]) {
+          const float rs = 1.0f / sqrtf(ss[h] / (float)HDQ + ea.eps);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) v[nb][r] = (v[nb][r] * rs) * nwv[nb][r];
+          for (int b = 0; b < NBH; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[h * NBH + b][r] = (v[h * NBH + b][r] * rs) * nwv[h * NBH + b][r];
         }
       }
     }
     if constexpr (EPI == EPI_BIAS_GELU) {
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[nb][r] = gelu_erf(v[nb][r]);
     }
@@ -246,7 +326,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
       int64_t orow = m;
       if constexpr (EPI == EPI_SCATTER_RESIDUAL) orow = ea.geom.token_of_row(m);
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
+      for (int nb = 0; nb < NB; ++nb) {
         const int n = nw0 + nb * 16 + fg * 4;
         if (n < N) {
           if constexpr (EPI == EPI_BIAS_RESIDUAL || EPI == EPI_SCATTER_RESIDUAL) {
@@ -270,6 +350,8 @@ static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t
   NSW_CHECK_ARG(K % KT == 0, "%s: K=%lld must be a multiple of %d", what, (long long)K, KT);
   NSW_CHECK_ARG(N % 4 == 0, "%s: N=%lld must be a multiple of 4", what, (long long)N);
   NSW_CHECK_ARG(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31), "%s: dims too large", what);
+  NSW_CHECK_ARG((uint64_t)M * K * sizeof(T) < (1ULL << 31) && (uint64_t)N * K * sizeof(T) < (1ULL << 31),
+                "%s: operands above 2 GiB are not supported (32-bit buffer offsets)", what);
   NSW_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)y % 8) == 0,
                 "%s: x and w must be 16-byte aligned, y 8-byte aligned", what);
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
@@ -301,8 +383,10 @@ int gemm_qkv(const void* x, const void* wqkv, const void* bqkv, const void* qn_w
                 (long long)hd);
   NSW_CHECK_ARG(bqkv && qn_w && kn_w, "%s: bias and norm weights are required", what);
   EpiArgs ea{};
-  ea.bias = bqkv; ea.qn_w = qn_w; ea.kn_w = kn_w; ea.eps = eps; ea.C = (int)C; ea.hd = (int)hd;
-  return dispatch_gemm<EPI_QKV_HEADNORM>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
+  ea.bias = bqkv; ea.qn_w = qn_w; ea.kn_w = kn_w; ea.eps = eps; ea.C = (int)C;
+  if (hd == 64) return dispatch_gemm<EPI_QKV_HN64>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
+  if (hd == 32) return dispatch_gemm<EPI_QKV_HN32>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
+  return dispatch_gemm<EPI_QKV_HN16>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
 }
 
 int gemm_proj_scatter(const void* o, const void* wproj, const void* bproj, const void* skip, void* y,
