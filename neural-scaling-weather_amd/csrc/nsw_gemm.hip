@@ -8,16 +8,18 @@
 // of 64 bytes per row (32 bf16 / 16 f32) for the 256 x-rows and 256 w-rows
 // (32 KB).  Global -> LDS copies use gfx950's buffer_load_dwordx4 ... lds
 // (direct to LDS, no VGPR staging): each instruction writes 1 KB = 16 rows of
-// one wave's share.  Rows are XOR-swizzled in 16-byte chunks
-// (slot = chunk ^ ((row >> 2) & 3)) so that the 16-lane phases of the
-// fragment reads (16 rows, same chunk) hit 16 distinct bank groups.
+// one wave's share.  Rows are XOR-swizzled in 16-byte chunks,
+// slot = chunk ^ g(row), g(r) = ((r >> 1) ^ (r >> 3)) & 3, so that a fragment
+// read (16 rows, same chunk) is bank-conflict free whether ds_read_b128 is
+// served in 8-lane phases over 32 banks or 16-lane phases over 64 banks.
 //
-// Pipeline per k tile kt: wait for this wave's copies of tile kt+1, barrier,
-// issue the copies of tile kt+3 into the stage freed by tile kt-1, then run
-// the 64 MFMAs of tile kt from registers while the 16 fragment reads of tile
-// kt+1 are interleaved between them (register double buffering).  The
-// barrier is a bare s_barrier: __syncthreads() would add a fence that waits
-// for every outstanding copy.
+// Pipeline per k tile kt: wait for this wave's copies of tile kt+1 and its
+// fragment reads of tile kt, barrier, issue the copies of tile kt+4 into the
+// stage of tile kt (its fragments are in registers by then: prefetch distance
+// 3 tiles with 4 stages), then run the 64 MFMAs of tile kt from registers
+// while the 16 fragment reads of tile kt+1 are interleaved between them
+// (register double buffering).  The barrier is a bare s_barrier:
+// __syncthreads() would add a fence that waits for every outstanding copy.
 //
 // The MFMA is issued "transposed": the A operand is the weight fragment
 // (rows n) and the B operand the activation fragment (rows m), so lane l of a
@@ -62,6 +64,7 @@ constexpr int ROWB = 64;            // k-tile bytes per row
 constexpr int NSTAGE = 4;           // LDS ring depth
 constexpr int STAGE_BYTES = (BM + BN) * ROWB;          // 32 KB
 constexpr int COPIES = STAGE_BYTES / (256 * 16);       // 16-byte copies per thread per tile (8)
+static_assert(COPIES == MB, "one copy instruction is issued per 8-MFMA group");
 
 struct EpiArgs {
   const void* bias;
@@ -116,37 +119,70 @@ __device__ __forceinline__ int xcd_remap(int bid, int ntiles) {
   return x * q + (x < rem ? x : rem) + idx;
 }
 
-// Buffer resource over a whole tensor (raw buffer, 32-bit byte offsets).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+// Buffer resource (V#) over a whole tensor: raw buffer, stride 0, 32-bit
+// byte offsets, num_records = bytes, dword 3 = 0x00020000 (the gfx9 raw
+// buffer format).  Built from wave-uniform values so it lives in SGPRs.
+__device__ __forceinline__ u32x4 make_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = (uint64_t)p;
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
+// One direct-to-LDS copy: every lane loads 16 bytes at rsrc + voff + soff and
+// the wave's 64 x 16 B land contiguously at LDS byte address lds_addr.
+// Issued as inline asm so that the compiler's wait-count insertion does not
+// see an LDS write in flight (it would otherwise drain all copies before
+// each fragment read); ordering is kept by the explicit vmcnt waits and
+// barriers of the pipeline.  s_nop: M0 write -> LDS-DMA read hazard.
+__device__ __forceinline__ void dma16(const u32x4& rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "m0");
+}
+
+// Barrier between waves with no fence (a fence would wait for every copy)
+// and compiler-level memory ordering on both sides.
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // s_waitcnt vmcnt(N) only (expcnt / lgkmcnt fields at their "no wait" maxima).
 #define NSW_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
+// s_waitcnt lgkmcnt(0) only.
+#define NSW_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
+
+// Swizzle of a 64-byte row (4 chunks of 16 B).
+__device__ __forceinline__ int row_swizzle(int row) {
+  const int r = row & 15;   // position inside the 16-row block
+  return ((r >> 1) ^ (r >> 3)) & 3;
+}
 
 // One 16-row x 16-byte-chunk slab per copy instruction: wave w, copy j covers
 // stage rows (w*COPIES + j)*16 .. +15; lane i writes row +i/4, slot i%4 and
-// therefore loads global chunk (i%4) ^ ((i/16)%4).
+// therefore loads global chunk (i%4) ^ row_swizzle(i/4).
 struct CopyPlan {
-  __amdgpu_buffer_rsrc_t rsrc;  // x for waves 0-1, w for waves 2-3 (wave-uniform)
+  u32x4 rsrc;                   // x for waves 0-1, w for waves 2-3 (wave-uniform)
   uint32_t voff[COPIES];        // byte offset of this lane's chunk at k tile 0
   int lds_row0;                 // first stage row of copy 0 for this wave
 };
 
+// Copy instruction j of k tile kt into `stage`.
+__device__ __forceinline__ void copy_slab(const CopyPlan& cp, char* stage, int j, int kt) {
+  dma16(cp.rsrc, (uint32_t)(uintptr_t)(stage + (cp.lds_row0 + j * 16) * ROWB), cp.voff[j], kt * ROWB);
+}
+
 template <typename T>
 __device__ __forceinline__ void issue_tile(const CopyPlan& cp, char* stage, int kt) {
 #pragma unroll
-  for (int j = 0; j < COPIES; ++j)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(cp.rsrc, (lds_ptr_t)(stage + (cp.lds_row0 + j * 16) * ROWB), 16,
-                                             cp.voff[j], kt * ROWB, 0, 0);
+  for (int j = 0; j < COPIES; ++j) copy_slab(cp, stage, j, kt);
 }
 
 // Fragment reads of one k tile: W rows (A operand) and X rows (B operand).
 __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int fg) {
-  const int slot = fg ^ ((row >> 2) & 3);
+  const int slot = fg ^ row_swizzle(row);
   return *reinterpret_cast<const u32x4*>(stage + row * ROWB + slot * 16);
 }
 
@@ -179,7 +215,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
   cp.rsrc = xside ? make_rsrc(X, (uint32_t)M * rowbytes) : make_rsrc(Wt, (uint32_t)N * rowbytes);
   cp.lds_row0 = wave * COPIES * 16;
   {
-    const int chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    const int chunk = (lane & 3) ^ row_swizzle(lane >> 2);
 #pragma unroll
     for (int j = 0; j < COPIES; ++j) {
       const int srow = cp.lds_row0 + j * 16 + (lane >> 2);
@@ -203,31 +239,46 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
 
   u32x4 fa[2][NB], fb[2][MB];
 
-  // prologue: tiles 0..2 in flight, wait for tile 0, read its fragments
+  // prologue: tiles 0..3 in flight, wait for tile 0, read its fragments
   issue_tile<T>(cp, lds0, 0);
   if (nk > 1) issue_tile<T>(cp, lds1, 1);
   if (nk > 2) issue_tile<T>(cp, lds2, 2);
-  if (nk > 2) NSW_WAIT_VMCNT(2 * COPIES);
+  if (nk > 3) issue_tile<T>(cp, lds3, 3);
+  if (nk > 3) NSW_WAIT_VMCNT(3 * COPIES);
+  else if (nk > 2) NSW_WAIT_VMCNT(2 * COPIES);
   else if (nk > 1) NSW_WAIT_VMCNT(COPIES);
   else NSW_WAIT_VMCNT(0);
-  __builtin_amdgcn_s_barrier();
+  wg_barrier();
 #pragma unroll
   for (int i = 0; i < NB; ++i) fa[0][i] = lds_frag(lds0, arow + i * 16, fg);
 #pragma unroll
   for (int i = 0; i < MB; ++i) fb[0][i] = lds_frag(lds0, brow + i * 16, fg);
 
-  // one k tile: U = position in the 4-stage ring (compile time), k = kt + U
-#define NSW_STEP(U, CUR, NXT, ISS)                                                             \
+  // One k tile, U = position in the ring (compile time), k = kt + U.
+  //   1. wait for this wave's copies of tile k+1 (tiles k+2, k+3 may still
+  //      be in flight) and for its own fragment reads of tile k;
+  //   2. barrier: tile k+1 is in LDS for every wave and no wave still reads
+  //      stage CUR, so
+  //   3. tile k+4 is copied into CUR (prefetch distance 3 tiles), one of the
+  //      8 copy instructions per 8 MFMAs (issued in a burst they stall the
+  //      wave on the address unit), while
+  //   4. the 64 MFMAs of tile k run from registers with the 16 fragment
+  //      reads of tile k+1 (stage NXT) interleaved.
+#define NSW_STEP(U, CUR, NXT)                                                                  \
   {                                                                                            \
     const int k = kt + U;                                                                      \
     if (k < nk) {                                                                              \
       if (k + 1 < nk) {                                                                        \
-        if (k + 2 < nk) NSW_WAIT_VMCNT(COPIES); else NSW_WAIT_VMCNT(0);                        \
-        __builtin_amdgcn_s_barrier();                                                          \
+        const int ahead = min(nk - 1, k + 3) - (k + 1);                                        \
+        if (ahead >= 2) NSW_WAIT_VMCNT(2 * COPIES);                                            \
+        else if (ahead == 1) NSW_WAIT_VMCNT(COPIES);                                           \
+        else NSW_WAIT_VMCNT(0);                                                                \
+        NSW_WAIT_LGKMCNT0();                                                                   \
+        wg_barrier();                                                                          \
       }                                                                                        \
-      if (k + 3 < nk) issue_tile<T>(cp, ISS, k + 3);                                           \
       const char* nx = (k + 1 < nk) ? NXT : CUR;                                               \
       _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                      \
+        if (k + 4 < nk) copy_slab(cp, CUR, mb, k + 4);                                         \
         fb[(U + 1) & 1][mb] = lds_frag(nx, brow + mb * 16, fg);                                \
         fa[(U + 1) & 1][mb] = lds_frag(nx, arow + mb * 16, fg);                                \
         _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                      \
@@ -239,10 +290,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
   }
 
   for (int kt = 0; kt < nk; kt += NSTAGE) {
-    NSW_STEP(0, lds0, lds1, lds3)
-    NSW_STEP(1, lds1, lds2, lds0)
-    NSW_STEP(2, lds2, lds3, lds1)
-    NSW_STEP(3, lds3, lds0, lds2)
+    NSW_STEP(0, lds0, lds1)
+    NSW_STEP(1, lds1, lds2)
+    NSW_STEP(2, lds2, lds3)
+    NSW_STEP(3, lds3, lds0)
   }
 #undef NSW_STEP
 
