@@ -66,7 +66,20 @@ def main():
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy (5 launches): the reference kernel whose "
+                         "FETCH_SIZE / WRITE_SIZE counters calibrate the HBM-traffic figures")
     args = ap.parse_args()
+
+    if args.copy_calibration:
+        import torch
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": src.numel(), "launches": 5}), flush=True)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -205,21 +218,24 @@ def cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, target_s):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     p = {k: v.detach().float().cpu() for k, v in blk.state_dict().items()}
-    nb = 1
     g = torch.Generator().manual_seed(7)
-    times = []
+    # size the sample: one band first, then as many bands as make a run of
+    # ~target_s/5 seconds (at most the whole image), repeated to ~target_s
+    x1 = torch.randn(B, T, ws[0], W, C, generator=g)
+    swin_ref.block_forward(x1, p, heads, ws, shift)  # warm-up
+    t0 = time.perf_counter()
+    swin_ref.block_forward(x1, p, heads, ws, shift)
+    t1 = time.perf_counter() - t0
+    nbands = H // ws[0]
+    nb = max(1, min(nbands, int(round(target_s / 5.0 / max(t1, 1e-3)))))
     Hs = ws[0] * nb
     xs = torch.randn(B, T, Hs, W, C, generator=g)
-    swin_ref.block_forward(xs, p, heads, ws, shift)  # warm-up
-    t_first = None
+    times = []
     while True:
         t0 = time.perf_counter()
         swin_ref.block_forward(xs, p, heads, ws, shift)
-        dt = time.perf_counter() - t0
-        times.append(dt)
-        if t_first is None:
-            t_first = dt
-        if sum(times) >= target_s or len(times) >= 10:
+        times.append(time.perf_counter() - t0)
+        if sum(times) >= target_s or len(times) >= 20:
             break
     med = statistics.median(times)
     toks = B * T * Hs * W
@@ -234,7 +250,7 @@ def cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, target_s):
         pass
     return {"value": round(toks / med, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"fp32 oracle block (oracle/swin_ref.py, eager torch) on {nb} latitude band "
+            "sample": f"fp32 oracle block (oracle/swin_ref.py, eager torch) on {nb} of {nbands} latitude bands "
                       f"({Hs}x{W} tokens = {toks}, C={C}), median of {len(times)} runs "
                       f"({med:.2f} s each); cpu: {cpu_model}"}
 
