@@ -55,16 +55,44 @@ constexpr int qkv_head_dim(int epi) {
 }
 
 constexpr int BM = 256;             // activation rows (m) per workgroup tile
-constexpr int BN = 256;             // weight rows (n) per workgroup tile
 constexpr int WTM = 128;            // wave tile (m)
-constexpr int WTN = 128;            // wave tile (n)
 constexpr int MB = WTM / 16;        // 16x16 result blocks per wave along m
-constexpr int NB = WTN / 16;        // ... along n
 constexpr int ROWB = 64;            // k-tile bytes per row
-constexpr int NSTAGE = 4;           // LDS ring depth
-constexpr int STAGE_BYTES = (BM + BN) * ROWB;          // 32 KB
-constexpr int COPIES = STAGE_BYTES / (256 * 16);       // 16-byte copies per thread per tile (8)
-static_assert(COPIES == MB, "one copy instruction is issued per 8-MFMA group");
+constexpr int SLABS_X = BM / 16;    // 16-row slabs of x per stage
+
+// Two tile configurations (template parameter TN = weight rows per tile):
+//   TN = 256: 256 x 256 tile, 4 waves of 128 x 128, 4-stage ring (128 KB),
+//             one workgroup per CU — the better main loop, used for long K;
+//   TN = 128: 256 x 128 tile, 4 waves of 128 x 64, 3-stage ring (72 KB), two
+//             workgroups per CU, so that one tile's prologue, barriers and
+//             epilogue overlap the other's MFMAs — used for K <= 2048, where
+//             those fixed costs are a larger share.
+template <int TN> struct Cfg {
+  static constexpr int BN = TN;                         // weight rows (n) per tile
+  static constexpr int WTN = TN / 2;                    // wave tile (n)
+  static constexpr int NB = WTN / 16;                   // 16x16 blocks per wave along n
+  static constexpr int NSTAGE = TN == 256 ? 4 : 3;      // LDS ring depth
+  static constexpr int WG_PER_CU = TN == 256 ? 1 : 2;
+  static constexpr int UNROLL = NSTAGE % 2 == 0 ? NSTAGE : 2 * NSTAGE;  // ring x fragment buffers
+  static constexpr int STAGE_BYTES = (BM + BN) * ROWB;  // 32 / 24 KB
+  static constexpr int COPIES = STAGE_BYTES / (256 * 16);  // 16-byte copies per thread per tile (8 / 6)
+  static_assert(COPIES <= MB, "copy instructions are spread over the 8-MFMA groups of a tile");
+};
+
+// epilogue staging of the output tile in LDS, in the output dtype: the whole
+// 256-row tile when it fits in the workgroup's share of the CU's 160 KB,
+// else two halves; rows padded by 16 B so that the fragment-layout writes
+// spread over the banks
+template <typename T, int TN> struct Stg {
+  static constexpr int BUDGET = 160 * 1024 / Cfg<TN>::WG_PER_CU;
+  static constexpr int RING = Cfg<TN>::NSTAGE * Cfg<TN>::STAGE_BYTES;
+  static constexpr int STRIDE = TN * (int)sizeof(T) + 16;
+  static constexpr int ROWS = BM * STRIDE <= BUDGET ? BM : BM / 2;
+  static constexpr int PASSES = BM / ROWS;
+  static constexpr int BYTES = ROWS * STRIDE;
+  static constexpr int SMEM = RING > BYTES ? RING : BYTES;
+  static_assert(SMEM <= BUDGET, "LDS use exceeds the workgroup's share of the CU");
+};
 
 struct EpiArgs {
   const void* bias;
@@ -161,21 +189,24 @@ __device__ __forceinline__ int row_swizzle(int row) {
 }
 
 // One 16-row x 16-byte-chunk slab per copy instruction: wave w, copy j covers
-// stage rows (w*COPIES + j)*16 .. +15; lane i writes row +i/4, slot i%4 and
-// therefore loads global chunk (i%4) ^ row_swizzle(i/4).
+// stage rows (w*COPIES + j)*16 .. +15 (x rows first, then w rows); lane i
+// writes row +i/4, slot i%4 and therefore loads global chunk
+// (i%4) ^ row_swizzle(i/4).
+template <int COPIES>
 struct CopyPlan {
-  u32x4 rsrc;                   // x for waves 0-1, w for waves 2-3 (wave-uniform)
+  u32x4 rsrc[COPIES];           // x or w buffer per copy (wave-uniform)
   uint32_t voff[COPIES];        // byte offset of this lane's chunk at k tile 0
   int lds_row0;                 // first stage row of copy 0 for this wave
 };
 
 // Copy instruction j of k tile kt into `stage`.
-__device__ __forceinline__ void copy_slab(const CopyPlan& cp, char* stage, int j, int kt) {
-  dma16(cp.rsrc, (uint32_t)(uintptr_t)(stage + (cp.lds_row0 + j * 16) * ROWB), cp.voff[j], kt * ROWB);
+template <int COPIES>
+__device__ __forceinline__ void copy_slab(const CopyPlan<COPIES>& cp, char* stage, int j, int kt) {
+  dma16(cp.rsrc[j], (uint32_t)(uintptr_t)(stage + (cp.lds_row0 + j * 16) * ROWB), cp.voff[j], kt * ROWB);
 }
 
-template <typename T>
-__device__ __forceinline__ void issue_tile(const CopyPlan& cp, char* stage, int kt) {
+template <int COPIES>
+__device__ __forceinline__ void issue_tile(const CopyPlan<COPIES>& cp, char* stage, int kt) {
 #pragma unroll
   for (int j = 0; j < COPIES; ++j) copy_slab(cp, stage, j, kt);
 }
@@ -186,17 +217,22 @@ __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int fg) {
   return *reinterpret_cast<const u32x4*>(stage + row * ROWB + slot * 16);
 }
 
-template <typename T, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, const T* __restrict__ Wt,
-                                                   T* __restrict__ Y, int M, int N, int K,
-                                                   EpiArgs ea) {
+template <typename T, int EPI, int TN>
+__global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* __restrict__ X,
+                                                                      const T* __restrict__ Wt,
+                                                                      T* __restrict__ Y, int M, int N,
+                                                                      int K, EpiArgs ea) {
   constexpr int KT = ROWB / sizeof(T);       // elements per k tile
-  // four separate arrays (not one) so that the compiler's wait-count
-  // tracking can tell the stages' direct-to-LDS copies apart
-  __shared__ __attribute__((aligned(1024))) char lds0[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) char lds1[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) char lds2[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) char lds3[STAGE_BYTES];
+  constexpr int BN = Cfg<TN>::BN;
+  constexpr int WTN = Cfg<TN>::WTN;
+  constexpr int NB = Cfg<TN>::NB;
+  constexpr int NSTAGE = Cfg<TN>::NSTAGE;
+  constexpr int UNROLL = Cfg<TN>::UNROLL;
+  constexpr int STAGE_BYTES = Cfg<TN>::STAGE_BYTES;
+  constexpr int COPIES = Cfg<TN>::COPIES;
+  // the 4-stage operand ring during the k loop, the output staging area in
+  // the epilogue
+  __shared__ __attribute__((aligned(1024))) char smem[Stg<T, TN>::SMEM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -208,16 +244,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
   const int mt = tile / NT, nt = tile - mt * NT;
   const int m0 = mt * BM, n0 = nt * BN;
 
-  // ---- copy plan: waves 0-1 stage the 256 x rows, waves 2-3 the 256 w rows
+  // ---- copy plan: the stage holds the BM x rows, then the BN w rows
   const uint32_t rowbytes = (uint32_t)K * sizeof(T);
-  CopyPlan cp;
-  const bool xside = wave < 2;
-  cp.rsrc = xside ? make_rsrc(X, (uint32_t)M * rowbytes) : make_rsrc(Wt, (uint32_t)N * rowbytes);
+  CopyPlan<COPIES> cp;
+  const u32x4 rx = make_rsrc(X, (uint32_t)M * rowbytes);
+  const u32x4 rw = make_rsrc(Wt, (uint32_t)N * rowbytes);
   cp.lds_row0 = wave * COPIES * 16;
   {
     const int chunk = (lane & 3) ^ row_swizzle(lane >> 2);
 #pragma unroll
     for (int j = 0; j < COPIES; ++j) {
+      const bool xside = wave * COPIES + j < SLABS_X;   // wave-uniform
+      cp.rsrc[j] = xside ? rx : rw;
       const int srow = cp.lds_row0 + j * 16 + (lane >> 2);
       int g = xside ? m0 + srow : n0 + srow - BM;
       const int lim = xside ? M : N;
@@ -239,63 +277,76 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
 
   u32x4 fa[2][NB], fb[2][MB];
 
-  // prologue: tiles 0..3 in flight, wait for tile 0, read its fragments
-  issue_tile<T>(cp, lds0, 0);
-  if (nk > 1) issue_tile<T>(cp, lds1, 1);
-  if (nk > 2) issue_tile<T>(cp, lds2, 2);
-  if (nk > 3) issue_tile<T>(cp, lds3, 3);
-  if (nk > 3) NSW_WAIT_VMCNT(3 * COPIES);
-  else if (nk > 2) NSW_WAIT_VMCNT(2 * COPIES);
-  else if (nk > 1) NSW_WAIT_VMCNT(COPIES);
-  else NSW_WAIT_VMCNT(0);
+#define NSW_STAGE(i) (smem + ((i) % NSTAGE) * STAGE_BYTES)
+  // wait until at most `ahead` younger tiles' copies of this wave are in flight
+#define NSW_WAIT_AHEAD(ahead)                                                                  \
+  do {                                                                                         \
+    const int a_ = (ahead);                                                                    \
+    if (a_ >= 3) NSW_WAIT_VMCNT(3 * COPIES);                                                   \
+    else if (a_ == 2) NSW_WAIT_VMCNT(2 * COPIES);                                              \
+    else if (a_ == 1) NSW_WAIT_VMCNT(COPIES);                                                  \
+    else NSW_WAIT_VMCNT(0);                                                                    \
+  } while (0)
+
+  // prologue: tiles 0..NSTAGE-1 in flight, wait for tile 0, read its fragments
+#pragma unroll
+  for (int t = 0; t < NSTAGE; ++t)
+    if (t < nk) issue_tile<COPIES>(cp, NSW_STAGE(t), t);
+  NSW_WAIT_AHEAD(min(nk - 1, NSTAGE - 1));
   wg_barrier();
 #pragma unroll
-  for (int i = 0; i < NB; ++i) fa[0][i] = lds_frag(lds0, arow + i * 16, fg);
+  for (int i = 0; i < NB; ++i) fa[0][i] = lds_frag(NSW_STAGE(0), arow + i * 16, fg);
 #pragma unroll
-  for (int i = 0; i < MB; ++i) fb[0][i] = lds_frag(lds0, brow + i * 16, fg);
+  for (int i = 0; i < MB; ++i) fb[0][i] = lds_frag(NSW_STAGE(0), brow + i * 16, fg);
 
-  // One k tile, U = position in the ring (compile time), k = kt + U.
-  //   1. wait for this wave's copies of tile k+1 (tiles k+2, k+3 may still
-  //      be in flight) and for its own fragment reads of tile k;
+  // One k tile, U = position in the unrolled ring (compile time), k = kt + U.
+  //   1. wait for this wave's copies of tile k+1 (younger tiles may still be
+  //      in flight) and for its own fragment reads of tile k;
   //   2. barrier: tile k+1 is in LDS for every wave and no wave still reads
-  //      stage CUR, so
-  //   3. tile k+4 is copied into CUR (prefetch distance 3 tiles), one of the
-  //      8 copy instructions per 8 MFMAs (issued in a burst they stall the
-  //      wave on the address unit), while
-  //   4. the 64 MFMAs of tile k run from registers with the 16 fragment
-  //      reads of tile k+1 (stage NXT) interleaved.
-#define NSW_STEP(U, CUR, NXT)                                                                  \
+  //      the stage of tile k, so
+  //   3. tile k+NSTAGE is copied into that stage (one copy instruction per
+  //      8-MFMA group: issued in a burst they stall the wave on the address
+  //      unit), while
+  //   4. the MFMAs of tile k run from registers with the fragment reads of
+  //      tile k+1 interleaved.
+#define NSW_STEP(U)                                                                            \
   {                                                                                            \
     const int k = kt + U;                                                                      \
     if (k < nk) {                                                                              \
+      char* const cur = NSW_STAGE(U);                                                          \
       if (k + 1 < nk) {                                                                        \
-        const int ahead = min(nk - 1, k + 3) - (k + 1);                                        \
-        if (ahead >= 2) NSW_WAIT_VMCNT(2 * COPIES);                                            \
-        else if (ahead == 1) NSW_WAIT_VMCNT(COPIES);                                           \
-        else NSW_WAIT_VMCNT(0);                                                                \
+        NSW_WAIT_AHEAD(min(nk - 1, k + NSTAGE - 1) - (k + 1));                                 \
         NSW_WAIT_LGKMCNT0();                                                                   \
         wg_barrier();                                                                          \
       }                                                                                        \
-      const char* nx = (k + 1 < nk) ? NXT : CUR;                                               \
+      const char* nx = (k + 1 < nk) ? NSW_STAGE(U + 1) : cur;                                  \
       _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                      \
-        if (k + 4 < nk) copy_slab(cp, CUR, mb, k + 4);                                         \
+        if (mb < COPIES && k + NSTAGE < nk) copy_slab(cp, cur, mb, k + NSTAGE);                \
         fb[(U + 1) & 1][mb] = lds_frag(nx, brow + mb * 16, fg);                                \
-        fa[(U + 1) & 1][mb] = lds_frag(nx, arow + mb * 16, fg);                                \
+        if (mb < NB) fa[(U + 1) & 1][mb] = lds_frag(nx, arow + mb * 16, fg);                   \
         _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                      \
           mfma_chunk<T>(acc[nb][mb], fa[U & 1][nb], fb[U & 1][mb]);                            \
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                                     \
+        if (mb < NB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                        \
+        else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                \
         __builtin_amdgcn_sched_group_barrier(0x008, NB * (sizeof(T) == 2 ? 1 : 4), 0);         \
       }                                                                                        \
     }                                                                                          \
   }
 
-  for (int kt = 0; kt < nk; kt += NSTAGE) {
-    NSW_STEP(0, lds0, lds1)
-    NSW_STEP(1, lds1, lds2)
-    NSW_STEP(2, lds2, lds3)
-    NSW_STEP(3, lds3, lds0)
+  for (int kt = 0; kt < nk; kt += UNROLL) {
+    NSW_STEP(0)
+    NSW_STEP(1)
+    NSW_STEP(2)
+    NSW_STEP(3)
+    if constexpr (UNROLL == 6) {
+      NSW_STEP(4)
+      NSW_STEP(5)
+    }
   }
 #undef NSW_STEP
+#undef NSW_WAIT_AHEAD
+#undef NSW_STAGE
+  static_assert(UNROLL == 4 || UNROLL == 6, "the k loop above is unrolled by hand for 4 or 6 steps");
 
   // ---------------------------------------------------------------- epilogue
   // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
@@ -334,9 +385,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
     }
   }
 
+  // 1. epilogue math in the fragment layout, in place
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
-    const int m = m0 + wm * WTM + mb * 16 + frow;
     float v[NB][4];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -373,24 +424,93 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ X, cons
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[nb][r] = gelu_erf(v[nb][r]);
     }
-    if (m < M) {
-      int64_t orow = m;
-      if constexpr (EPI == EPI_SCATTER_RESIDUAL) orow = ea.geom.token_of_row(m);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int n = nw0 + nb * 16 + fg * 4;
-        if (n < N) {
-          if constexpr (EPI == EPI_BIAS_RESIDUAL || EPI == EPI_SCATTER_RESIDUAL) {
-            float rv[4];
-            load4<T>((const T*)ea.residual + orow * N + n, rv);
+    for (int nb = 0; nb < NB; ++nb) acc[nb][mb] = f32x4{v[nb][0], v[nb][1], v[nb][2], v[nb][3]};
+  }
+
+  // 2. write-out through LDS: the waves owning the staged rows store their
+  // values in the fragment layout (output dtype), then every wave copies
+  // whole rows out with 16-byte lane accesses (fully coalesced), adding the
+  // residual there.  The residual rows are loaded before the barrier so that
+  // their latency overlaps the staging.
+  using S = Stg<T, TN>;
+  constexpr int VEC = 16 / sizeof(T);                 // elements per 16-byte chunk
+  constexpr int LPR = BN / VEC;                       // lanes per output row (32 bf16 / 64 f32)
+  constexpr int RPI = 64 / LPR;                       // rows per copy instruction (2 / 1)
+  constexpr int ITER = S::ROWS / 4 / RPI;             // copy instructions per wave per pass
+  constexpr bool RES = EPI == EPI_BIAS_RESIDUAL || EPI == EPI_SCATTER_RESIDUAL;
+  NSW_WAIT_LGKMCNT0();
+  wg_barrier();                                       // the operand ring is no longer read
+  char* stg = smem;
+  const int lrow = lane / LPR;                        // row of this lane within an instruction
+  const int col = (lane % LPR) * VEC;                 // first tile column of this lane
+  const int n = n0 + col;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[nb][r] += rv[r];
-          }
-          store4<T>(Y + orow * N + n, v[nb]);
+  for (int pass = 0; pass < S::PASSES; ++pass) {
+    const int prow0 = pass * S::ROWS;                 // first tile row of this pass
+    // residual prefetch for this wave's rows of the pass
+    u32x4 rres[RES ? ITER : 1];
+    if constexpr (RES) {
+#pragma unroll
+      for (int it = 0; it < ITER; ++it) {
+        const int rl = (wave * ITER + it) * RPI + lrow;
+        const int m = m0 + prow0 + rl;
+        rres[it] = u32x4{0u, 0u, 0u, 0u};
+        if (m < M && n < N) {
+          int64_t orow = m;
+          if constexpr (EPI == EPI_SCATTER_RESIDUAL) orow = ea.geom.token_of_row(m);
+          rres[it] = *reinterpret_cast<const u32x4*>((const T*)ea.residual + orow * N + n);
         }
       }
     }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int trow = wm * WTM + mb * 16 + frow - prow0;
+      if (trow >= 0 && trow < S::ROWS) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          float v4[4] = {acc[nb][mb][0], acc[nb][mb][1], acc[nb][mb][2], acc[nb][mb][3]};
+          store4<T>(reinterpret_cast<T*>(stg + trow * S::STRIDE) + wn * WTN + nb * 16 + fg * 4, v4);
+        }
+      }
+    }
+    wg_barrier();
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+      const int rl = (wave * ITER + it) * RPI + lrow;
+      const int m = m0 + prow0 + rl;
+      if (m < M && n < N) {
+        int64_t orow = m;
+        if constexpr (EPI == EPI_SCATTER_RESIDUAL) orow = ea.geom.token_of_row(m);
+        float o[VEC];
+        load16<T>(reinterpret_cast<const T*>(stg + rl * S::STRIDE) + col, o);
+        if constexpr (RES) {
+          float rv[VEC];
+          if constexpr (sizeof(T) == 2) {
+            const bf16x8 rb = __builtin_bit_cast(bf16x8, rres[it]);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) rv[e] = (float)rb[e];
+          } else {
+            const f32x4 rf = __builtin_bit_cast(f32x4, rres[it]);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) rv[e] = rf[e];
+          }
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[e] += rv[e];
+        }
+        store16<T>(Y + orow * N + n, o);
+      }
+    }
+    if (pass + 1 < S::PASSES) wg_barrier();          // before the next pass overwrites the staging rows
   }
+}
+
+template <typename T, int EPI, int TN>
+static void launch_tiles(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
+                         const EpiArgs& ea, hipStream_t st) {
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + TN - 1) / TN);
+  hipLaunchKernelGGL((gemm_kernel<T, EPI, TN>), dim3((unsigned)tiles), dim3(256), 0, st, (const T*)x,
+                     (const T*)w, (T*)y, (int)M, (int)N, (int)K, ea);
 }
 
 template <typename T, int EPI>
@@ -399,16 +519,16 @@ static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t
   constexpr int KT = ROWB / sizeof(T);
   NSW_CHECK_ARG(M > 0 && N > 0 && K > 0, "%s: M, N, K must be positive", what);
   NSW_CHECK_ARG(K % KT == 0, "%s: K=%lld must be a multiple of %d", what, (long long)K, KT);
-  NSW_CHECK_ARG(N % 4 == 0, "%s: N=%lld must be a multiple of 4", what, (long long)N);
+  NSW_CHECK_ARG(N % 8 == 0, "%s: N=%lld must be a multiple of 8", what, (long long)N);
   NSW_CHECK_ARG(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31), "%s: dims too large", what);
   NSW_CHECK_ARG((uint64_t)M * K * sizeof(T) < (1ULL << 31) && (uint64_t)N * K * sizeof(T) < (1ULL << 31),
                 "%s: operands above 2 GiB are not supported (32-bit buffer offsets)", what);
-  NSW_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)y % 8) == 0,
-                "%s: x and w must be 16-byte aligned, y 8-byte aligned", what);
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  NSW_CHECK_ARG(tiles < (1LL << 31), "%s: too many tiles", what);
-  hipLaunchKernelGGL((gemm_kernel<T, EPI>), dim3((unsigned)tiles), dim3(256), 0, st, (const T*)x,
-                     (const T*)w, (T*)y, (int)M, (int)N, (int)K, ea);
+  NSW_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)y % 16) == 0 &&
+                    ((uintptr_t)ea.residual % 16) == 0,
+                "%s: x, w, y and residual must be 16-byte aligned", what);
+  NSW_CHECK_ARG(((M + BM - 1) / BM) * ((N + 127) / 128) < (1LL << 31), "%s: too many tiles", what);
+  if (K > 2048) launch_tiles<T, EPI, 256>(x, w, y, M, N, K, ea, st);
+  else launch_tiles<T, EPI, 128>(x, w, y, M, N, K, ea, st);
   return check_launch(what);
 }
 
