@@ -6,9 +6,10 @@
 // padded to a multiple of 32 keys).  Each wavefront takes 16-query blocks and
 //   1. computes S^T = K Q^T with v_mfma_f32_16x16x32_bf16, so that lane l
 //      holds the logits of query l%16 for keys 16*kb + 4*(l/16) + r;
-//   2. adds the additive mask (the reference's latitude shift mask computed
-//      from indices, or a materialised mask), does the softmax in the exp2
-//      domain with two cross-lane shuffles per reduction;
+//   2. adds the additive mask (the reference's latitude shift mask, taken
+//      from a per-window key-class bit set built with one ballot per 64 keys,
+//      or a materialised mask), does the softmax in the exp2 domain with
+//      permlane row reductions;
 //   3. reuses the probability registers directly as the B operand of
 //      O^T = V^T P^T (the k order of a 32-key step is {4g+r, 16+4g+r} for lane
 //      group g; the V^T fragment is read from LDS in the same order), and
@@ -18,6 +19,8 @@
 // Generic path (attn_scalar_kernel, fp32 and any head dim): one thread per
 // query, online softmax over 64-key chunks staged in LDS, fp32 throughout.
 #include "nsw_common.h"
+
+#include <utility>
 
 namespace nsw {
 
@@ -57,127 +60,189 @@ __device__ __forceinline__ bool window_in_last_band(const AttnArgs& a, int64_t w
 }
 
 // ------------------------------------------------------------ bf16 MFMA ----
-template <int HD, int NKB>
-__global__ __launch_bounds__(256) void attn_mfma_kernel(AttnArgs a) {
+// NKB = ceil(L / 16) exactly, so only the last 16-key block holds padding.
+template <int HD, int NKB, bool MT>
+__global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
   constexpr int KP = ((NKB * 16 + 31) / 32) * 32;  // padded keys (multiple of 32)
   constexpr int KS_STRIDE = HD + 8;                // bf16 elements per K row in LDS
   constexpr int VT_STRIDE = KP + 4;                // bf16 elements per V^T row in LDS
   constexpr int NS = HD / 32;                      // k-steps of the QK^T product
   constexpr int NDB = HD / 16;                     // 16-wide head-dim blocks
   constexpr int NKS = KP / 32;                     // 32-key steps of PV
+  constexpr int CPR = HD / 8;                      // 16-byte chunks per K / V row
+  constexpr int NCH = (KP * CPR + 255) / 256;      // chunks staged per thread
+  constexpr int NCLS = (KP + 63) / 64;             // 64-bit words of the key-class set
   constexpr float LOG2E = 1.4426950408889634f;
   __shared__ __attribute__((aligned(16))) bf16 Ks[KP * KS_STRIDE];
   __shared__ __attribute__((aligned(16))) bf16 Vt[HD * VT_STRIDE];
+  __shared__ uint64_t cls[NCLS];
 
-  const int64_t win = blockIdx.x / a.heads;
-  const int head = blockIdx.x - (int)(win * a.heads);
+  const int win = (int)(blockIdx.x / (unsigned)a.heads);
+  const int head = (int)blockIdx.x - win * a.heads;
   const int L = a.L, C = a.C;
   const int64_t ld = 3 * (int64_t)C;
-  const bf16* base = (const bf16*)a.qkv + win * L * ld;
+  const bf16* base = (const bf16*)a.qkv + (int64_t)win * L * ld + head * HD;
   const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fg = lane >> 4;
 
-  // ---- stage K and V^T (zero padded)
-  constexpr int CPR = HD / 8;  // 16-byte chunks per row
-  for (int idx = tid; idx < KP * CPR; idx += 256) {
+  // Q fragments of this wave's first query block (issued before the staging
+  // so that their latency overlaps it).
+  bf16x8 qf[NS];
+  auto load_q = [&](int qb) {
+    const int q = qb * 16 + fr;
+    const int qc = q < L ? q : L - 1;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(base + qc * ld + 32 * s + 8 * fg);
+  };
+  if (wave < NKB) load_q(wave);
+
+  // ---- stage K and V^T (zero padded): all loads first, then the LDS stores
+  bf16x8 kv[NCH], vv[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int idx = tid + 256 * c;
     const int key = idx / CPR, ch = idx - key * CPR;
-    bf16x8 kv, vv;
-    if (key < L) {
-      const bf16* rowp = base + key * ld + head * HD + ch * 8;
-      kv = *reinterpret_cast<const bf16x8*>(rowp + C);
-      vv = *reinterpret_cast<const bf16x8*>(rowp + 2 * C);
+    if (idx < KP * CPR && key < L) {
+      const bf16* rowp = base + key * ld + ch * 8;
+      kv[c] = *reinterpret_cast<const bf16x8*>(rowp + C);
+      vv[c] = *reinterpret_cast<const bf16x8*>(rowp + 2 * C);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) { kv[e] = (bf16)0.f; vv[e] = (bf16)0.f; }
+      for (int e = 0; e < 8; ++e) { kv[c][e] = (bf16)0.f; vv[c][e] = (bf16)0.f; }
     }
-    *reinterpret_cast<bf16x8*>(&Ks[key * KS_STRIDE + ch * 8]) = kv;
+  }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VT_STRIDE + key] = vv[e];
+  for (int c = 0; c < NCH; ++c) {
+    const int idx = tid + 256 * c;
+    const int key = idx / CPR, ch = idx - key * CPR;
+    if (idx < KP * CPR) {
+      *reinterpret_cast<bf16x8*>(&Ks[key * KS_STRIDE + ch * 8]) = kv[c];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VT_STRIDE + key] = vv[c][e];
+    }
+  }
+  // Shift mask of a last-band window: key class = (row within the window)
+  // >= ws0 - s0; a query attends with -100 to keys of the other class.
+  const bool shifted = !MT && window_in_last_band(a, win);
+  if (shifted && wave == 0) {
+    const int thr = (a.g.ws0 - a.g.s0) * a.g.ws1;
+#pragma unroll
+    for (int w = 0; w < NCLS; ++w) {
+      const int key = 64 * w + lane;
+      const uint64_t b = __ballot(key < L && (key % a.g.wa) >= thr);
+      if (lane == 0) cls[w] = b;
+    }
   }
   __syncthreads();
 
-  const int lane = tid & 63, wave = tid >> 6;
-  const int fr = lane & 15, fg = lane >> 4;
-  const bool last_band = window_in_last_band(a, win);
+  // Additive masks are applied to the raw q.k products as mask / scale, so
+  // that one FMA per logit, p = exp2(s * scale*log2(e) - max), finishes it.
   const float zscale = a.scale * LOG2E;
-  const int nqb = (L + 15) / 16;
-  const int nkb = (L + 15) / 16;
+  const float smask = -100.0f / a.scale;
 
-  for (int qb = wave; qb < nqb; qb += 4) {
+  for (int qb = wave; qb < NKB; qb += 4) {
     const int q = qb * 16 + fr;
     const int qc = q < L ? q : L - 1;
-    bf16x8 qf[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-      qf[s] = *reinterpret_cast<const bf16x8*>(base + qc * ld + head * HD + 32 * s + 8 * fg);
-
+    // S^T = K Q^T; K fragments run KD 16-key blocks ahead of the MFMAs
+    constexpr int KD = NKB < 4 ? NKB : 4;
     f32x4 S[NKB];
+    bf16x8 kf[KD][NS];
+#pragma unroll
+    for (int kb = 0; kb < KD; ++kb)
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        kf[kb][s] = *reinterpret_cast<const bf16x8*>(&Ks[(kb * 16 + fr) * KS_STRIDE + 32 * s + 8 * fg]);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (kb < nkb) {
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[(kb * 16 + fr) * KS_STRIDE + 32 * s + 8 * fg]);
-          S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], S[kb], 0, 0, 0);
+      for (int s = 0; s < NS; ++s) S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb % KD][s], qf[s], S[kb], 0, 0, 0);
+      if (kb + KD < NKB) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          kf[kb % KD][s] =
+              *reinterpret_cast<const bf16x8*>(&Ks[((kb + KD) * 16 + fr) * KS_STRIDE + 32 * s + 8 * fg]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (qb + 4 < NKB) load_q(qb + 4);
+
+    // lane: query fr, keys 16*kb + 4*fg + r
+    if constexpr (MT) {
+      const float* mrow = a.mask + ((int64_t)(win % a.nW_mask) * L + qc) * (int64_t)L;
+      const float inv_scale = 1.0f / a.scale;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kb * 16 + 4 * fg + r;
+          if (kb < NKB - 1 || key < L) S[kb][r] += mrow[key] * inv_scale;
         }
+    } else if (shifted) {
+      const int qcls = (int)((cls[qc >> 6] >> (qc & 63)) & 1);
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const unsigned bits = (unsigned)(cls[kb >> 2] >> (16 * (kb & 3) + 4 * fg)) & 0xFu;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if ((int)((bits >> r) & 1u) != qcls) S[kb][r] += smask;
       }
     }
-    // logits in the log2 domain, mask, running max
-    float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
+    for (int r = 0; r < 4; ++r)
+      if ((NKB - 1) * 16 + 4 * fg + r >= L) S[NKB - 1][r] = -INFINITY;
+    float mx = S[0][0];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kb * 16 + 4 * fg + r;
-        float z = -INFINITY;
-        if (kb < nkb && key < L) {
-          z = S[kb][r] * zscale;
-          if (a.mask_mode != MASK_NONE) z += mask_value(a, win, qc, key, last_band) * LOG2E;
-        }
-        S[kb][r] = z;
-        mx = fmaxf(mx, z);
-      }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[kb][r]);
+    mx = rows4_max(mx);
+    const float off = -mx * zscale;
     float sum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = exp2f(S[kb][r] - mx);
+        const float p = __builtin_amdgcn_exp2f(fmaf(S[kb][r], zscale, off));
         S[kb][r] = p;
         sum += p;
       }
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
+    sum = rows4_sum(sum);
 
-    // O^T = V^T P^T
+    // O^T = V^T P^T; V^T fragments double-buffered across 32-key steps
     f32x4 O[NDB];
 #pragma unroll
     for (int db = 0; db < NDB; ++db) O[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x4 vf[2][NDB][2];
+    auto load_v = [&](int buf, int ks) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const bf16* vrow = &Vt[(db * 16 + fr) * VT_STRIDE + 32 * ks + 4 * fg];
+        vf[buf][db][0] = *reinterpret_cast<const bf16x4*>(vrow);
+        vf[buf][db][1] = *reinterpret_cast<const bf16x4*>(vrow + 16);
+      }
+    };
+    load_v(0, 0);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
-      if (2 * ks < nkb) {
-        bf16x8 pf;
+      if (ks + 1 < NKS) load_v((ks + 1) & 1, ks + 1);
+      bf16x8 pf;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pf[r] = (bf16)S[2 * ks][r];
-          pf[4 + r] = (2 * ks + 1 < NKB) ? (bf16)S[2 * ks + 1][r] : (bf16)0.f;
-        }
+      for (int r = 0; r < 4; ++r) {
+        pf[r] = (bf16)S[2 * ks][r];
+        pf[4 + r] = (2 * ks + 1 < NKB) ? (bf16)S[2 * ks + 1][r] : (bf16)0.f;
+      }
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const bf16* vrow = &Vt[(db * 16 + fr) * VT_STRIDE + 32 * ks + 4 * fg];
-          bf16x4 v0 = *reinterpret_cast<const bf16x4*>(vrow);
-          bf16x4 v1 = *reinterpret_cast<const bf16x4*>(vrow + 16);
-          bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-          O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, O[db], 0, 0, 0);
-        }
+      for (int db = 0; db < NDB; ++db) {
+        const bf16x4 v0 = vf[ks & 1][db][0], v1 = vf[ks & 1][db][1];
+        const bf16x8 v = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, pf, O[db], 0, 0, 0);
       }
     }
     if (q < L) {
       const float inv = 1.0f / sum;
-      bf16* orow = (bf16*)a.o + (win * L + q) * (int64_t)C + head * HD;
+      bf16* orow = (bf16*)a.o + ((int64_t)win * L + q) * (int64_t)C + head * HD;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
         float v[4] = {O[db][0] * inv, O[db][1] * inv, O[db][2] * inv, O[db][3] * inv};
@@ -250,16 +315,26 @@ __global__ __launch_bounds__(256) void attn_scalar_kernel(AttnArgs a) {
   }
 }
 
+template <int HD, int NKB>
+static void launch_nkb(const AttnArgs& a, int64_t grid, hipStream_t st) {
+  if (a.mask_mode == MASK_TENSOR)
+    hipLaunchKernelGGL((attn_mfma_kernel<HD, NKB, true>), dim3((unsigned)grid), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_mfma_kernel<HD, NKB, false>), dim3((unsigned)grid), dim3(256), 0, st, a);
+}
+
+// One instance per 16-key block count, L <= 384 (24 blocks).
+template <int HD, int... N>
+static int launch_mfma_seq(const AttnArgs& a, int64_t grid, hipStream_t st, std::integer_sequence<int, N...>) {
+  const int nkb = (a.L + 15) / 16;
+  bool done = false;
+  ((nkb == N + 1 ? (launch_nkb<HD, N + 1>(a, grid, st), done = true) : false), ...);
+  return done ? 0 : -1;
+}
+
 template <int HD>
 static int launch_mfma(const AttnArgs& a, int64_t grid, hipStream_t st) {
-  const int nkb = (a.L + 15) / 16;
-  if (nkb <= 4) hipLaunchKernelGGL((attn_mfma_kernel<HD, 4>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  else if (nkb <= 8) hipLaunchKernelGGL((attn_mfma_kernel<HD, 8>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  else if (nkb <= 11) hipLaunchKernelGGL((attn_mfma_kernel<HD, 11>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  else if (nkb <= 16) hipLaunchKernelGGL((attn_mfma_kernel<HD, 16>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  else if (nkb <= 24) hipLaunchKernelGGL((attn_mfma_kernel<HD, 24>), dim3((unsigned)grid), dim3(256), 0, st, a);
-  else return -1;
-  return 0;
+  return launch_mfma_seq<HD>(a, grid, st, std::make_integer_sequence<int, 24>{});
 }
 
 template <typename T>
