@@ -8,11 +8,12 @@
 //      holds the logits of query l%16 for keys 16*kb + 4*(l/16) + r;
 //   2. adds the additive mask (the reference's latitude shift mask, taken
 //      from a per-window key-class bit set built with one ballot per 64 keys,
-//      or a materialised mask), does the softmax in the exp2 domain with
-//      permlane row reductions;
+//      or a materialised mask), does the softmax in the exp2 domain (row max
+//      by permlane reduction, row sum by the PV MFMA against a ones block);
 //   3. reuses the probability registers directly as the B operand of
 //      O^T = V^T P^T (the k order of a 32-key step is {4g+r, 16+4g+r} for lane
-//      group g; the V^T fragment is read from LDS in the same order), and
+//      group g; V^T is stored with its keys in that order, so each A fragment
+//      is one 16-byte LDS read), and
 //   4. writes O[q][h*hd + d] with one 8-byte store per 4 head dims.
 // Padding keys get -inf logits; no FLOPs are counted for them.
 //
@@ -60,12 +61,21 @@ __device__ __forceinline__ bool window_in_last_band(const AttnArgs& a, int64_t w
 }
 
 // ------------------------------------------------------------ bf16 MFMA ----
+// Column of key k in a V^T row.  Within each 32-key step the keys are stored
+// in the order the probability registers hold them: lane group g carries keys
+// 4g..4g+3 and 16+4g..16+4g+3, so position 8g + 4h + r holds key 16h + 4g + r
+// and each lane reads its 8 V^T values with one 16-byte LDS read.
+__device__ __forceinline__ int vt_pos(int k) {
+  const int j = k & 31;
+  return (k & ~31) | ((j & 15) >> 2) << 3 | (j >> 4) << 2 | (j & 3);
+}
+
 // NKB = ceil(L / 16) exactly, so only the last 16-key block holds padding.
 template <int HD, int NKB, bool MT>
 __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
   constexpr int KP = ((NKB * 16 + 31) / 32) * 32;  // padded keys (multiple of 32)
   constexpr int KS_STRIDE = HD + 8;                // bf16 elements per K row in LDS
-  constexpr int VT_STRIDE = KP + 4;                // bf16 elements per V^T row in LDS
+  constexpr int VT_STRIDE = KP + 8;                // bf16 elements per V^T row (4 banks mod 64 dwords)
   constexpr int NS = HD / 32;                      // k-steps of the QK^T product
   constexpr int NDB = HD / 16;                     // 16-wide head-dim blocks
   constexpr int NKS = KP / 32;                     // 32-key steps of PV
@@ -86,16 +96,17 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
   const int lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fg = lane >> 4;
 
-  // Q fragments of this wave's first query block (issued before the staging
-  // so that their latency overlaps it).
-  bf16x8 qf[NS];
-  auto load_q = [&](int qb) {
-    const int q = qb * 16 + fr;
+  // Q fragments of all of this wave's query blocks (wave, wave + 4, ...),
+  // issued before the staging so that their latency overlaps it.
+  constexpr int QPW = (NKB + 3) / 4;
+  bf16x8 qf[QPW][NS];
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int q = (wave + 4 * i) * 16 + fr;
     const int qc = q < L ? q : L - 1;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(base + qc * ld + 32 * s + 8 * fg);
-  };
-  if (wave < NKB) load_q(wave);
+    for (int s = 0; s < NS; ++s) qf[i][s] = *reinterpret_cast<const bf16x8*>(base + qc * ld + 32 * s + 8 * fg);
+  }
 
   // ---- stage K and V^T (zero padded): all loads first, then the LDS stores
   bf16x8 kv[NCH], vv[NCH];
@@ -118,8 +129,9 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
     const int key = idx / CPR, ch = idx - key * CPR;
     if (idx < KP * CPR) {
       *reinterpret_cast<bf16x8*>(&Ks[key * KS_STRIDE + ch * 8]) = kv[c];
+      const int kpos = vt_pos(key);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VT_STRIDE + key] = vv[c][e];
+      for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VT_STRIDE + kpos] = vv[c][e];
     }
   }
   // Shift mask of a last-band window: key class = (row within the window)
@@ -141,7 +153,10 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
   const float zscale = a.scale * LOG2E;
   const float smask = -100.0f / a.scale;
 
-  for (int qb = wave; qb < NKB; qb += 4) {
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int qb = wave + 4 * i;
+    if (qb >= NKB) break;
     const int q = qb * 16 + fr;
     const int qc = q < L ? q : L - 1;
     // S^T = K Q^T; K fragments run KD 16-key blocks ahead of the MFMAs
@@ -157,7 +172,7 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
     for (int kb = 0; kb < NKB; ++kb) {
       S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < NS; ++s) S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb % KD][s], qf[s], S[kb], 0, 0, 0);
+      for (int s = 0; s < NS; ++s) S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb % KD][s], qf[i][s], S[kb], 0, 0, 0);
       if (kb + KD < NKB) {
 #pragma unroll
         for (int s = 0; s < NS; ++s)
@@ -166,7 +181,6 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (qb + 4 < NKB) load_q(qb + 4);
 
     // lane: query fr, keys 16*kb + 4*fg + r
     if constexpr (MT) {
@@ -199,29 +213,23 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[kb][r]);
     mx = rows4_max(mx);
     const float off = -mx * zscale;
-    float sum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(S[kb][r], zscale, off));
-        S[kb][r] = p;
-        sum += p;
-      }
-    sum = rows4_sum(sum);
+      for (int r = 0; r < 4; ++r) S[kb][r] = __builtin_amdgcn_exp2f(fmaf(S[kb][r], zscale, off));
 
-    // O^T = V^T P^T; V^T fragments double-buffered across 32-key steps
-    f32x4 O[NDB];
+    // O^T = V^T P^T; V^T fragments double-buffered across 32-key steps.  An
+    // extra all-ones A block gives the row sums of the (bf16) probabilities
+    // on every lane of the query, the same values that weight V.
+    f32x4 O[NDB], Z = {0.f, 0.f, 0.f, 0.f};
+    const bf16x8 ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
 #pragma unroll
     for (int db = 0; db < NDB; ++db) O[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    bf16x4 vf[2][NDB][2];
+    bf16x8 vf[2][NDB];
     auto load_v = [&](int buf, int ks) {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const bf16* vrow = &Vt[(db * 16 + fr) * VT_STRIDE + 32 * ks + 4 * fg];
-        vf[buf][db][0] = *reinterpret_cast<const bf16x4*>(vrow);
-        vf[buf][db][1] = *reinterpret_cast<const bf16x4*>(vrow + 16);
-      }
+      for (int db = 0; db < NDB; ++db)
+        vf[buf][db] = *reinterpret_cast<const bf16x8*>(&Vt[(db * 16 + fr) * VT_STRIDE + 32 * ks + 8 * fg]);
     };
     load_v(0, 0);
 #pragma unroll
@@ -235,13 +243,12 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
       }
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const bf16x4 v0 = vf[ks & 1][db][0], v1 = vf[ks & 1][db][1];
-        const bf16x8 v = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v, pf, O[db], 0, 0, 0);
+        O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[ks & 1][db], pf, O[db], 0, 0, 0);
       }
+      Z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, Z, 0, 0, 0);
     }
     if (q < L) {
-      const float inv = 1.0f / sum;
+      const float inv = 1.0f / Z[0];
       bf16* orow = (bf16*)a.o + ((int64_t)win * L + q) * (int64_t)C + head * HD;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
