@@ -95,7 +95,7 @@ int nsw_rmsnorm_roll_partition(const void* x, const void* w, float eps, void* xw
 /* F.linear + BiasLayer (+ GELU / residual) (models/layer_helpers.py:41-42,71-72,
  * models/mlp.py:80-93): y[M,N] = epi(x[M,K] . w[N,K]^T).  bias / residual may
  * be NULL when the epilogue does not use them.  Requires K % 64 == 0 (bf16) or
- * K % 32 == 0 (f32), N % 4 == 0. */
+ * K % 32 == 0 (f32), N % 8 == 0, 16-byte aligned x, w, y and residual. */
 int nsw_linear(const void* x, const void* w, const void* bias, const void* residual, void* y,
                int64_t M, int64_t N, int64_t K, int epilogue, int dtype, void* stream);
 

@@ -1,31 +1,41 @@
 // MFMA GEMM y[M,N] = epilogue(x[M,K] . w[N,K]^T) for gfx950, with the Swin
 // block's epilogues fused in.
 //
-// Workgroup tile 256 (m) x 256 (n), 4 wavefronts, each owning a 128 x 128
-// sub-tile = 8 x 8 blocks of 16x16 fp32 accumulators (256 AGPRs per lane).
+// Workgroup tile 256 (m) x TN (n), 4 wavefronts in a 2 x 2 grid, each owning
+// a 128 x TN/2 sub-tile of 16x16 fp32 accumulator blocks.  Two
+// configurations (Cfg<TN>):
+//   TN = 256: one workgroup per CU, LDS stages of 128 bytes of k per row
+//             (64 bf16) for the 256 x-rows and 256 w-rows (64 KB), 2 stages;
+//   TN = 128: two workgroups per CU, stages of 64 bytes of k per row (24 KB),
+//             3 stages, so that one tile's epilogue overlaps the other's
+//             MFMAs (short K with a GELU, head-norm or scatter epilogue).
+// A stage of 128-byte rows is consumed as two MFMA steps of 32 bf16; its
+// copies read whole 128-byte lines, half as many line requests per byte as
+// 64-byte rows.
 //
-// Operand staging: a ring of NSTAGE = 4 LDS stages, each holding one k tile
-// of 64 bytes per row (32 bf16 / 16 f32) for the 256 x-rows and 256 w-rows
-// (32 KB).  Global -> LDS copies use gfx950's buffer_load_dwordx4 ... lds
-// (direct to LDS, no VGPR staging): each instruction writes 1 KB = 16 rows of
-// one wave's share.  Rows are XOR-swizzled in 16-byte chunks,
-// slot = chunk ^ g(row), g(r) = ((r >> 1) ^ (r >> 3)) & 3, so that a fragment
-// read (16 rows, same chunk) is bank-conflict free whether ds_read_b128 is
-// served in 8-lane phases over 32 banks or 16-lane phases over 64 banks.
+// Operand staging: global -> LDS copies use gfx950's buffer_load_dwordx4 ...
+// lds (direct to LDS, no VGPR staging): each instruction writes 1 KB = 1024 /
+// ROWB stage rows of one wave's share.  Rows are XOR-swizzled in 16-byte
+// chunks so that a fragment read (16 rows, same chunk) is bank-conflict free
+// whether ds_read_b128 is served in 8-lane phases over 32 banks or 16-lane
+// phases over 64 banks: slot = chunk ^ g(row & 15) with
+//   64-byte rows:  g(r) = ((r >> 1) ^ (r >> 3)) & 3,
+//   128-byte rows: g(r) = ((r >> 1) & 7) ^ ((r & 1) << 2).
 //
-// Pipeline per k tile kt: wait for this wave's copies of tile kt+1 and its
-// fragment reads of tile kt, barrier, issue the copies of tile kt+4 into the
-// stage of tile kt (its fragments are in registers by then: prefetch distance
-// 3 tiles with 4 stages), then run the 64 MFMAs of tile kt from registers
-// while the 16 fragment reads of tile kt+1 are interleaved between them
-// (register double buffering).  The barrier is a bare s_barrier:
-// __syncthreads() would add a fence that waits for every outstanding copy.
+// Pipeline per MFMA step k (32 bf16 of k): when step k+1 starts a new stage,
+// wait for this wave's copies of that stage and its own fragment reads, then
+// barrier; the stage of step k is then free and the copies of stage
+// k/SUB + NSTAGE are issued into it, spread over the step's MFMA groups.  The
+// MFMAs of step k run from registers while the fragment reads of step k+1 are
+// interleaved between them (register double buffering).  The barrier is a
+// bare s_barrier: __syncthreads() would add a fence that waits for every
+// outstanding copy.
 //
 // The MFMA is issued "transposed": the A operand is the weight fragment
 // (rows n) and the B operand the activation fragment (rows m), so lane l of a
 // 16x16 result block holds y[m = l%16][n = 4*(l/16) + r], r = 0..3: four
-// consecutive output columns, written as one 8-byte (bf16) / 16-byte (f32)
-// store, and a row's head-norm reduction needs only two cross-lane shuffles.
+// consecutive output columns, and a row's head-norm reduction needs only two
+// cross-lane permutes.
 //
 //   bf16: v_mfma_f32_16x16x32_bf16, one instruction per 16-byte fragment pair
 //   f32 : v_mfma_f32_16x16x4_f32, four instructions per 16-byte fragment pair
@@ -33,8 +43,9 @@
 //          the same assignment, so the k-sum is exact)
 //
 // Workgroups are remapped so that each XCD (8 on MI355X, dispatched
-// round-robin) works on a contiguous range of tiles, n fastest: the ~32 CUs of
-// an XCD share a few m-row panels of x and the whole w in their L2.
+// round-robin) works on a contiguous range of tiles, in groups of GROUP_M
+// row blocks x all column blocks (column-major inside a group), so that the
+// tiles in flight on an XCD share both row panels and weight panels in its L2.
 #include "nsw_common.h"
 
 namespace nsw {
@@ -57,26 +68,29 @@ constexpr int qkv_head_dim(int epi) {
 constexpr int BM = 256;             // activation rows (m) per workgroup tile
 constexpr int WTM = 128;            // wave tile (m)
 constexpr int MB = WTM / 16;        // 16x16 result blocks per wave along m
-constexpr int ROWB = 64;            // k-tile bytes per row
-constexpr int SLABS_X = BM / 16;    // 16-row slabs of x per stage
+constexpr int STEPB = 64;           // k bytes per row consumed by one MFMA step
 
 // Two tile configurations (template parameter TN = weight rows per tile):
-//   TN = 256: 256 x 256 tile, 4 waves of 128 x 128, 4-stage ring (128 KB),
-//             one workgroup per CU — the better main loop, used for long K;
-//   TN = 128: 256 x 128 tile, 4 waves of 128 x 64, 3-stage ring (72 KB), two
-//             workgroups per CU, so that one tile's prologue, barriers and
-//             epilogue overlap the other's MFMAs — used for K <= 2048, where
-//             those fixed costs are a larger share.
+//   TN = 256: 256 x 256 tile, 4 waves of 128 x 128, 2 stages of 128-byte
+//             rows (128 KB), one workgroup per CU;
+//   TN = 128: 256 x 128 tile, 4 waves of 128 x 64, 3 stages of 64-byte rows
+//             (72 KB), two workgroups per CU, so that one tile's prologue,
+//             barriers and epilogue overlap the other's MFMAs — measured
+//             best for short K (<= 2048) with a heavy epilogue (GELU, head
+//             norm, row scatter).
 template <int TN> struct Cfg {
   static constexpr int BN = TN;                         // weight rows (n) per tile
   static constexpr int WTN = TN / 2;                    // wave tile (n)
   static constexpr int NB = WTN / 16;                   // 16x16 blocks per wave along n
-  static constexpr int NSTAGE = TN == 256 ? 4 : 3;      // LDS ring depth
+  static constexpr int ROWB = TN == 256 ? 128 : 64;     // k bytes per row per LDS stage
+  static constexpr int SUB = ROWB / STEPB;              // MFMA steps per stage
+  static constexpr int RPC = 1024 / ROWB;               // stage rows per copy instruction
+  static constexpr int NSTAGE = TN == 256 ? 2 : 3;      // LDS ring depth (128 KB / 72 KB)
   static constexpr int WG_PER_CU = TN == 256 ? 1 : 2;
-  static constexpr int UNROLL = NSTAGE % 2 == 0 ? NSTAGE : 2 * NSTAGE;  // ring x fragment buffers
-  static constexpr int STAGE_BYTES = (BM + BN) * ROWB;  // 32 / 24 KB
-  static constexpr int COPIES = STAGE_BYTES / (256 * 16);  // 16-byte copies per thread per tile (8 / 6)
-  static_assert(COPIES <= MB, "copy instructions are spread over the 8-MFMA groups of a tile");
+  static constexpr int UNROLL = (SUB * NSTAGE) % 2 == 0 ? SUB * NSTAGE : 2 * SUB * NSTAGE;
+  static constexpr int STAGE_BYTES = (BM + BN) * ROWB;
+  static constexpr int COPIES = STAGE_BYTES / (256 * 16);  // 16-byte copies per thread per stage
+  static constexpr int CPG = (COPIES + MB - 1) / MB;       // copies per 8-MFMA group
 };
 
 // epilogue staging of the output tile in LDS, in the output dtype: the whole
@@ -140,7 +154,9 @@ __device__ __forceinline__ void mfma_chunk(f32x4& acc, const u32x4& a, const u32
 
 // Bijective remap of the hardware workgroup id so that XCD x (which receives
 // ids x, x+8, x+16, ...) processes the contiguous logical range
-// [x*q + min(x, rem), ...).
+// [x*q + min(x, rem), ...); GROUP_M row blocks per tile group.
+constexpr int GROUP_M = 8;
+
 __device__ __forceinline__ int xcd_remap(int bid, int ntiles) {
   const int q = ntiles >> 3, rem = ntiles & 7;
   const int x = bid & 7, idx = bid >> 3;
@@ -182,38 +198,41 @@ __device__ __forceinline__ void wg_barrier() {
 // s_waitcnt lgkmcnt(0) only.
 #define NSW_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
 
-// Swizzle of a 64-byte row (4 chunks of 16 B).
+// Chunk swizzle of a stage row: 64 B (4 chunks) or 128 B (8 chunks).
+template <int ROWB>
 __device__ __forceinline__ int row_swizzle(int row) {
   const int r = row & 15;   // position inside the 16-row block
-  return ((r >> 1) ^ (r >> 3)) & 3;
+  if constexpr (ROWB == 64) return ((r >> 1) ^ (r >> 3)) & 3;
+  else return ((r >> 1) & 7) ^ ((r & 1) << 2);
 }
 
-// One 16-row x 16-byte-chunk slab per copy instruction: wave w, copy j covers
-// stage rows (w*COPIES + j)*16 .. +15 (x rows first, then w rows); lane i
-// writes row +i/4, slot i%4 and therefore loads global chunk
-// (i%4) ^ row_swizzle(i/4).
+// Copy instruction j of wave w covers stage rows (w*COPIES + j)*RPC .. +RPC-1
+// (x rows first, then w rows), RPC = 1024 / ROWB; lane i writes row
+// +i/(ROWB/16), slot i%(ROWB/16), and therefore loads global chunk
+// slot ^ row_swizzle(row).
 template <int COPIES>
 struct CopyPlan {
   u32x4 rsrc[COPIES];           // x or w buffer per copy (wave-uniform)
-  uint32_t voff[COPIES];        // byte offset of this lane's chunk at k tile 0
+  uint32_t voff[COPIES];        // byte offset of this lane's chunk at stage 0
   int lds_row0;                 // first stage row of copy 0 for this wave
 };
 
-// Copy instruction j of k tile kt into `stage`.
-template <int COPIES>
-__device__ __forceinline__ void copy_slab(const CopyPlan<COPIES>& cp, char* stage, int j, int kt) {
-  dma16(cp.rsrc[j], (uint32_t)(uintptr_t)(stage + (cp.lds_row0 + j * 16) * ROWB), cp.voff[j], kt * ROWB);
+// Copy instruction j of stage `st` (k bytes st*ROWB ..) into `stage`.
+template <int COPIES, int ROWB>
+__device__ __forceinline__ void copy_slab(const CopyPlan<COPIES>& cp, char* stage, int j, int st) {
+  dma16(cp.rsrc[j], (uint32_t)(uintptr_t)(stage + (cp.lds_row0 + j * (1024 / ROWB)) * ROWB), cp.voff[j], st * ROWB);
 }
 
-template <int COPIES>
-__device__ __forceinline__ void issue_tile(const CopyPlan<COPIES>& cp, char* stage, int kt) {
+template <int COPIES, int ROWB>
+__device__ __forceinline__ void issue_tile(const CopyPlan<COPIES>& cp, char* stage, int st) {
 #pragma unroll
-  for (int j = 0; j < COPIES; ++j) copy_slab(cp, stage, j, kt);
+  for (int j = 0; j < COPIES; ++j) copy_slab<COPIES, ROWB>(cp, stage, j, st);
 }
 
-// Fragment reads of one k tile: W rows (A operand) and X rows (B operand).
-__device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int fg) {
-  const int slot = fg ^ row_swizzle(row);
+// Fragment read: 16 bytes of k chunk `chunk` of a stage row.
+template <int ROWB>
+__device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk) {
+  const int slot = chunk ^ row_swizzle<ROWB>(row);
   return *reinterpret_cast<const u32x4*>(stage + row * ROWB + slot * 16);
 }
 
@@ -222,7 +241,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
                                                                       const T* __restrict__ Wt,
                                                                       T* __restrict__ Y, int M, int N,
                                                                       int K, EpiArgs ea) {
-  constexpr int KT = ROWB / sizeof(T);       // elements per k tile
+  constexpr int ROWB = Cfg<TN>::ROWB, SUB = Cfg<TN>::SUB, RPC = Cfg<TN>::RPC, CPG = Cfg<TN>::CPG;
   constexpr int BN = Cfg<TN>::BN;
   constexpr int WTN = Cfg<TN>::WTN;
   constexpr int NB = Cfg<TN>::NB;
@@ -240,8 +259,15 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   const int wm = wave >> 1, wn = wave & 1;
 
   const int MT = (M + BM - 1) / BM, NT = (N + BN - 1) / BN;
+  // Tiles of one XCD run in groups of GROUP_M row blocks x all column blocks,
+  // column-major inside the group, so that the tiles in flight on an XCD
+  // share both their row panels and their weight panels in its L2.
   const int tile = xcd_remap(blockIdx.x, MT * NT);
-  const int mt = tile / NT, nt = tile - mt * NT;
+  const int group = tile / (GROUP_M * NT);
+  const int gm0 = group * GROUP_M;
+  const int gsz = MT - gm0 < GROUP_M ? MT - gm0 : GROUP_M;
+  const int tin = tile - group * GROUP_M * NT;
+  const int mt = gm0 + tin % gsz, nt = tin / gsz;
   const int m0 = mt * BM, n0 = nt * BN;
 
   // ---- copy plan: the stage holds the BM x rows, then the BN w rows
@@ -249,14 +275,14 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   CopyPlan<COPIES> cp;
   const u32x4 rx = make_rsrc(X, (uint32_t)M * rowbytes);
   const u32x4 rw = make_rsrc(Wt, (uint32_t)N * rowbytes);
-  cp.lds_row0 = wave * COPIES * 16;
+  cp.lds_row0 = wave * COPIES * RPC;
   {
-    const int chunk = (lane & 3) ^ row_swizzle(lane >> 2);
 #pragma unroll
     for (int j = 0; j < COPIES; ++j) {
-      const bool xside = wave * COPIES + j < SLABS_X;   // wave-uniform
+      const bool xside = (wave * COPIES + j) * RPC < BM;   // wave-uniform
       cp.rsrc[j] = xside ? rx : rw;
-      const int srow = cp.lds_row0 + j * 16 + (lane >> 2);
+      const int srow = cp.lds_row0 + j * RPC + lane / (ROWB / 16);
+      const int chunk = (lane % (ROWB / 16)) ^ row_swizzle<ROWB>(srow);
       int g = xside ? m0 + srow : n0 + srow - BM;
       const int lim = xside ? M : N;
       g = g < lim ? g : lim - 1;   // rows past the edge re-read the last row (never stored)
@@ -273,12 +299,11 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   const int frow = lane & 15, fg = lane >> 4;
   const int arow = BM + wn * WTN + frow;   // w rows of this wave (A operand)
   const int brow = wm * WTM + frow;        // x rows of this wave (B operand)
-  const int nk = K / KT;
-
+  const int nk = K / (STEPB / (int)sizeof(T));   // MFMA steps
+  const int nst = nk / SUB;                       // LDS stages
   u32x4 fa[2][NB], fb[2][MB];
 
 #define NSW_STAGE(i) (smem + ((i) % NSTAGE) * STAGE_BYTES)
-  // wait until at most `ahead` younger tiles' copies of this wave are in flight
 #define NSW_WAIT_AHEAD(ahead)                                                                  \
   do {                                                                                         \
     const int a_ = (ahead);                                                                    \
@@ -288,42 +313,38 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
     else NSW_WAIT_VMCNT(0);                                                                    \
   } while (0)
 
-  // prologue: tiles 0..NSTAGE-1 in flight, wait for tile 0, read its fragments
 #pragma unroll
   for (int t = 0; t < NSTAGE; ++t)
-    if (t < nk) issue_tile<COPIES>(cp, NSW_STAGE(t), t);
-  NSW_WAIT_AHEAD(min(nk - 1, NSTAGE - 1));
+    if (t < nst) issue_tile<COPIES, ROWB>(cp, NSW_STAGE(t), t);
+  NSW_WAIT_AHEAD(min(nst - 1, NSTAGE - 1));
   wg_barrier();
 #pragma unroll
-  for (int i = 0; i < NB; ++i) fa[0][i] = lds_frag(NSW_STAGE(0), arow + i * 16, fg);
+  for (int i = 0; i < NB; ++i) fa[0][i] = lds_frag<ROWB>(NSW_STAGE(0), arow + i * 16, fg);
 #pragma unroll
-  for (int i = 0; i < MB; ++i) fb[0][i] = lds_frag(NSW_STAGE(0), brow + i * 16, fg);
+  for (int i = 0; i < MB; ++i) fb[0][i] = lds_frag<ROWB>(NSW_STAGE(0), brow + i * 16, fg);
 
-  // One k tile, U = position in the unrolled ring (compile time), k = kt + U.
-  //   1. wait for this wave's copies of tile k+1 (younger tiles may still be
-  //      in flight) and for its own fragment reads of tile k;
-  //   2. barrier: tile k+1 is in LDS for every wave and no wave still reads
-  //      the stage of tile k, so
-  //   3. tile k+NSTAGE is copied into that stage (one copy instruction per
-  //      8-MFMA group: issued in a burst they stall the wave on the address
-  //      unit), while
-  //   4. the MFMAs of tile k run from registers with the fragment reads of
-  //      tile k+1 interleaved.
 #define NSW_STEP(U)                                                                            \
   {                                                                                            \
     const int k = kt + U;                                                                      \
     if (k < nk) {                                                                              \
-      char* const cur = NSW_STAGE(U);                                                          \
-      if (k + 1 < nk) {                                                                        \
-        NSW_WAIT_AHEAD(min(nk - 1, k + NSTAGE - 1) - (k + 1));                                 \
+      constexpr int su_ = (U) / SUB, sn_ = ((U) + 1) / SUB;                                    \
+      constexpr bool bnd_ = ((U) + 1) % SUB == 0;                                              \
+      constexpr int nch_ = (((U) + 1) % SUB) * 4;                                              \
+      char* const cur = NSW_STAGE(su_);                                                        \
+      if (bnd_ && k + 1 < nk) {                                                                \
+        NSW_WAIT_AHEAD(min(nst - 1, NSTAGE - 1 + k / SUB) - (k + 1) / SUB);                    \
         NSW_WAIT_LGKMCNT0();                                                                   \
         wg_barrier();                                                                          \
       }                                                                                        \
-      const char* nx = (k + 1 < nk) ? NSW_STAGE(U + 1) : cur;                                  \
+      const char* nx = (k + 1 < nk) ? NSW_STAGE(sn_) : cur;                                    \
+      const int snext = k / SUB + NSTAGE;                                                      \
       _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                      \
-        if (mb < COPIES && k + NSTAGE < nk) copy_slab(cp, cur, mb, k + NSTAGE);                \
-        fb[(U + 1) & 1][mb] = lds_frag(nx, brow + mb * 16, fg);                                \
-        if (mb < NB) fa[(U + 1) & 1][mb] = lds_frag(nx, arow + mb * 16, fg);                   \
+        if (bnd_ && snext < nst) {                                                             \
+          _Pragma("unroll") for (int c_ = 0; c_ < CPG; ++c_)                                   \
+            if (mb * CPG + c_ < COPIES) copy_slab<COPIES, ROWB>(cp, cur, mb * CPG + c_, snext); \
+        }                                                                                      \
+        fb[(U + 1) & 1][mb] = lds_frag<ROWB>(nx, brow + mb * 16, nch_ + fg);                   \
+        if (mb < NB) fa[(U + 1) & 1][mb] = lds_frag<ROWB>(nx, arow + mb * 16, nch_ + fg);      \
         _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                      \
           mfma_chunk<T>(acc[nb][mb], fa[U & 1][nb], fb[U & 1][mb]);                            \
         if (mb < NB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                        \
@@ -338,15 +359,19 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
     NSW_STEP(1)
     NSW_STEP(2)
     NSW_STEP(3)
-    if constexpr (UNROLL == 6) {
+    if constexpr (UNROLL >= 6) {
       NSW_STEP(4)
       NSW_STEP(5)
+    }
+    if constexpr (UNROLL >= 8) {
+      NSW_STEP(6)
+      NSW_STEP(7)
     }
   }
 #undef NSW_STEP
 #undef NSW_WAIT_AHEAD
 #undef NSW_STAGE
-  static_assert(UNROLL == 4 || UNROLL == 6, "the k loop above is unrolled by hand for 4 or 6 steps");
+  static_assert(UNROLL % 2 == 0 && UNROLL <= 8, "unroll");
 
   // ---------------------------------------------------------------- epilogue
   // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
@@ -516,7 +541,7 @@ static void launch_tiles(const void* x, const void* w, void* y, int64_t M, int64
 template <typename T, int EPI>
 static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
                        const EpiArgs& ea, hipStream_t st, const char* what) {
-  constexpr int KT = ROWB / sizeof(T);
+  constexpr int KT = 128 / sizeof(T);
   NSW_CHECK_ARG(M > 0 && N > 0 && K > 0, "%s: M, N, K must be positive", what);
   NSW_CHECK_ARG(K % KT == 0, "%s: K=%lld must be a multiple of %d", what, (long long)K, KT);
   NSW_CHECK_ARG(N % 8 == 0, "%s: N=%lld must be a multiple of 8", what, (long long)N);
@@ -527,8 +552,12 @@ static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t
                     ((uintptr_t)ea.residual % 16) == 0,
                 "%s: x, w, y and residual must be 16-byte aligned", what);
   NSW_CHECK_ARG(((M + BM - 1) / BM) * ((N + 127) / 128) < (1LL << 31), "%s: too many tiles", what);
-  if (K > 2048) launch_tiles<T, EPI, 256>(x, w, y, M, N, K, ea, st);
-  else launch_tiles<T, EPI, 128>(x, w, y, M, N, K, ea, st);
+  // Short K with a heavy epilogue (GELU, head norm, row scatter): 256x128,
+  // two workgroups per CU overlap one tile's epilogue with the other's MFMAs.
+  // Otherwise the 256x256 main loop.
+  constexpr bool heavy = EPI == EPI_BIAS_GELU || EPI == EPI_SCATTER_RESIDUAL || qkv_head_dim(EPI) > 0;
+  if (heavy && K <= 2048) launch_tiles<T, EPI, 128>(x, w, y, M, N, K, ea, st);
+  else launch_tiles<T, EPI, 256>(x, w, y, M, N, K, ea, st);
   return check_launch(what);
 }
 
