@@ -176,6 +176,39 @@ int nsw_weighted_metrics(const float* pred, const float* target, const double* w
                          int64_t Cch, double* rmse, double* acc, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* The same metrics on unnormalised fields (the inference loop,
+ * utils/inferencer.py:390-391,405-412): pred (fp32 or bf16, pred_dtype) and
+ * target (fp32) are both mapped x -> x * std_c[c] + mean_c[c] (product and sum
+ * rounded separately, as the reference's two tensor ops) before the
+ * reduction.  std_c / mean_c fp32 [Cch]; workspace as above. */
+int nsw_weighted_metrics_unnorm(const void* pred, int pred_dtype, const float* target,
+                                const float* std_c, const float* mean_c, const double* w,
+                                int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
+                                int64_t Cch, double* rmse, double* acc, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/* Patch matrix of the stride-p patch convolution (PatchEmbedLayer,
+ * models/layer_helpers.py:120-172, as called by SwinTransformer.prepare_tokens,
+ * models/swin.py:269-277, and for the coordinate embedding, :278-282).
+ * x [B, T, C_x, H, W] (x_dtype); inv [C_inv, H, W] or NULL appended as extra
+ * channels (the preprocessor's concatenation, utils/data_utils.py:185-189);
+ * frame t is read from slot (t + frame0) mod T (a ring-buffered input
+ * window, utils/inferencer.py:448-449).  out [B*T*(H/p)*(W/p), Kp]
+ * (out_dtype), row (b, t, i, j), column (c*p + u)*p + v, zero for columns
+ * >= (C_x + C_inv)*p*p.  Requires p | H, p | W, p <= 16, Kp a multiple of 8
+ * (bf16) / 4 (f32), 16-byte aligned out. */
+int nsw_patch_im2col(const void* x, const void* inv, int64_t B, int64_t T, int64_t C_x,
+                     int64_t C_inv, int64_t H, int64_t W, int64_t p, int64_t frame0, int64_t Kp,
+                     void* out, int x_dtype, int out_dtype, void* stream);
+
+/* Head layout of SwinTransformer.forward_head (models/swin.py:293-299) for
+ * one frame: y [B*(H/p)*(W/p), p*p*C_out] (in_dtype), row (b, i, j), column
+ * (u*p + v)*C_out + c -> out[b*out_bstride + (c*H + i*p + u)*W + j*p + v]
+ * (out_dtype).  Requires p | H, p | W, p <= 16, p*p*C_out a multiple of 8
+ * (bf16) / 4 (f32), 16-byte aligned y. */
+int nsw_unpatchify(const void* y, void* out, int64_t B, int64_t C_out, int64_t H, int64_t W,
+                   int64_t p, int64_t out_bstride, int in_dtype, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,22 +18,37 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 }
 
 // FULLW: weights are a [H, W] map instead of one value per latitude row.
-template <bool VEC4, bool ACC, bool FULLW>
-__global__ __launch_bounds__(256) void wsum_partial_kernel(const float* __restrict__ pred,
+// TP: prediction dtype (float, or bf16 for a model's raw output).
+// AFFINE: both fields are first unnormalised per channel, x * std + mean,
+// rounded after the product and after the sum as the reference's two
+// separate tensor ops do (utils/inferencer.py:390-391,408-409).
+template <typename TP, bool VEC4, bool ACC, bool FULLW, bool AFFINE>
+__global__ __launch_bounds__(256) void wsum_partial_kernel(const TP* __restrict__ pred,
                                                            const float* __restrict__ tgt,
                                                            const double* __restrict__ wlat,
-                                                           const float* __restrict__ clim, int H,
+                                                           const float* __restrict__ clim,
+                                                           const float* __restrict__ std_c,
+                                                           const float* __restrict__ mean_c, int H,
                                                            int W, int Cch, int rpc, int nchunk,
                                                            double* __restrict__ partial) {
   const int64_t plane = blockIdx.x / nchunk;
   const int ch = blockIdx.x - (int)(plane * nchunk);
   const int h0 = ch * rpc;
   const int h1 = min(H, h0 + rpc);
-  const float cl = ACC ? clim[plane % Cch] : 0.f;
-  const float* pp = pred + plane * (int64_t)H * W;
+  const int cidx = (int)(plane % Cch);
+  const float cl = ACC ? clim[cidx] : 0.f;
+  const float sc = AFFINE ? std_c[cidx] : 1.f;
+  const float of = AFFINE ? mean_c[cidx] : 0.f;
+  const TP* pp = pred + plane * (int64_t)H * W;
   const float* tp = tgt + plane * (int64_t)H * W;
   double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
   auto acc1 = [&](float p, float t, double w) {
+    if constexpr (AFFINE) {
+      // two roundings, never an FMA (the device default contracts a*b+c)
+#pragma clang fp contract(off)
+      p = p * sc + of;
+      t = t * sc + of;
+    }
     const float d = p - t;
     const float d2 = d * d;
     s0 += w * (double)d2;
@@ -52,7 +67,8 @@ __global__ __launch_bounds__(256) void wsum_partial_kernel(const float* __restri
       const int x4 = (int)(i - (int64_t)hr * wq);
       const int h = h0 + hr;
       const int64_t off = (int64_t)h * W + 4 * x4;
-      const f32x4 p = *reinterpret_cast<const f32x4*>(pp + off);
+      float p[4];
+      load4<TP>(pp + off, p);
       const f32x4 t = *reinterpret_cast<const f32x4*>(tp + off);
       if constexpr (FULLW) {
         acc1(p[0], t[0], wlat[off]); acc1(p[1], t[1], wlat[off + 1]);
@@ -68,7 +84,7 @@ __global__ __launch_bounds__(256) void wsum_partial_kernel(const float* __restri
       const int hr = (int)(i / W);
       const int h = h0 + hr;
       const int64_t off = (int64_t)h * W + (i - (int64_t)hr * W);
-      acc1(pp[off], tp[off], FULLW ? wlat[off] : wlat[h]);
+      acc1(to_f32(pp[off]), tp[off], FULLW ? wlat[off] : wlat[h]);
     }
   }
   __shared__ double red[4][4];
@@ -116,47 +132,73 @@ extern "C" size_t nsw_weighted_metrics_workspace_size(int64_t P, int64_t H, int6
   return (size_t)P * nchunk * 4 * sizeof(double);
 }
 
-template <bool FULLW>
-static void launch_partial(bool vec4, bool acc, dim3 grid, hipStream_t st, const float* pred,
-                           const float* target, const double* w, const float* clim, int H, int W,
-                           int Cch, int rpc, int nchunk, double* partial) {
+template <typename TP, bool FULLW, bool AFFINE>
+static void launch_partial(bool vec4, bool acc, dim3 grid, hipStream_t st, const TP* pred,
+                           const float* target, const double* w, const float* clim, const float* sc,
+                           const float* of, int H, int W, int Cch, int rpc, int nchunk, double* partial) {
   dim3 block(256);
-  if (vec4 && acc)
-    hipLaunchKernelGGL((wsum_partial_kernel<true, true, FULLW>), grid, block, 0, st, pred, target, w, clim, H, W, Cch, rpc, nchunk, partial);
-  else if (vec4)
-    hipLaunchKernelGGL((wsum_partial_kernel<true, false, FULLW>), grid, block, 0, st, pred, target, w, clim, H, W, Cch, rpc, nchunk, partial);
-  else if (acc)
-    hipLaunchKernelGGL((wsum_partial_kernel<false, true, FULLW>), grid, block, 0, st, pred, target, w, clim, H, W, Cch, rpc, nchunk, partial);
+#define NSW_PARTIAL(V4, AC)                                                                             \
+  hipLaunchKernelGGL((wsum_partial_kernel<TP, V4, AC, FULLW, AFFINE>), grid, block, 0, st, pred, target, \
+                     w, clim, sc, of, H, W, Cch, rpc, nchunk, partial)
+  if (vec4 && acc) NSW_PARTIAL(true, true);
+  else if (vec4) NSW_PARTIAL(true, false);
+  else if (acc) NSW_PARTIAL(false, true);
+  else NSW_PARTIAL(false, false);
+#undef NSW_PARTIAL
+}
+
+template <typename TP, bool AFFINE>
+static int run_metrics(const TP* pred, const float* target, const double* w, int64_t w_cols,
+                       const float* clim, const float* sc, const float* of, int64_t P, int64_t H,
+                       int64_t W, int64_t Cch, double* rmse, double* acc, void* workspace,
+                       size_t workspace_bytes, hipStream_t st, const char* what) {
+  NSW_CHECK_ARG(P > 0 && H > 0 && W > 0 && Cch > 0, "%s: P, H, W, Cch must be positive", what);
+  NSW_CHECK_ARG(w_cols == 1 || w_cols == W, "%s: weights must be [H] / [H,1] or [H,W]", what);
+  NSW_CHECK_ARG(P % Cch == 0, "%s: P=%lld is not a multiple of Cch=%lld", what, (long long)P, (long long)Cch);
+  NSW_CHECK_ARG(H * W < (1LL << 31), "%s: plane too large", what);
+  NSW_CHECK_ARG(rmse != nullptr && (clim == nullptr || acc != nullptr), "%s: missing output", what);
+  NSW_CHECK_ARG(!AFFINE || (sc != nullptr && of != nullptr), "%s: std and mean are required", what);
+  const size_t need = nsw_weighted_metrics_workspace_size(P, H, W);
+  NSW_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "%s: workspace of %zu bytes needed", what, need);
+  int rpc, nchunk;
+  metrics_chunks(P, H, &rpc, &nchunk);
+  NSW_CHECK_ARG(P * nchunk < (1LL << 31), "%s: too many planes", what);
+  double* partial = (double*)workspace;
+  const bool vec4 = (W % 4 == 0) && ((uintptr_t)pred % (4 * sizeof(TP)) == 0) && ((uintptr_t)target % 16 == 0);
+  dim3 grid((unsigned)(P * nchunk));
+  if (w_cols == 1 || W == 1)
+    launch_partial<TP, false, AFFINE>(vec4, clim != nullptr, grid, st, pred, target, w, clim, sc, of, (int)H,
+                                      (int)W, (int)Cch, rpc, nchunk, partial);
   else
-    hipLaunchKernelGGL((wsum_partial_kernel<false, false, FULLW>), grid, block, 0, st, pred, target, w, clim, H, W, Cch, rpc, nchunk, partial);
+    launch_partial<TP, true, AFFINE>(vec4, clim != nullptr, grid, st, pred, target, w, clim, sc, of, (int)H,
+                                     (int)W, (int)Cch, rpc, nchunk, partial);
+  int rc = check_launch(what);
+  if (rc) return rc;
+  hipLaunchKernelGGL(wsum_final_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, st, partial, P,
+                     nchunk, (double)(H * W), clim != nullptr, rmse, acc);
+  return check_launch(what);
 }
 
 extern "C" int nsw_weighted_metrics(const float* pred, const float* target, const double* w,
                                     int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
                                     int64_t Cch, double* rmse, double* acc, void* workspace,
                                     size_t workspace_bytes, void* stream) {
-  const char* what = "nsw_weighted_metrics";
-  NSW_CHECK_ARG(P > 0 && H > 0 && W > 0 && Cch > 0, "%s: P, H, W, Cch must be positive", what);
-  NSW_CHECK_ARG(w_cols == 1 || w_cols == W, "%s: weights must be [H] / [H,1] or [H,W]", what);
-  NSW_CHECK_ARG(P % Cch == 0, "%s: P=%lld is not a multiple of Cch=%lld", what, (long long)P, (long long)Cch);
-  NSW_CHECK_ARG(H * W < (1LL << 31), "%s: plane too large", what);
-  NSW_CHECK_ARG(rmse != nullptr && (clim == nullptr || acc != nullptr), "%s: missing output", what);
-  const size_t need = nsw_weighted_metrics_workspace_size(P, H, W);
-  NSW_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "%s: workspace of %zu bytes needed", what, need);
-  int rpc, nchunk;
-  metrics_chunks(P, H, &rpc, &nchunk);
-  NSW_CHECK_ARG(P * nchunk < (1LL << 31), "%s: too many planes", what);
+  return run_metrics<float, false>(pred, target, w, w_cols, clim, nullptr, nullptr, P, H, W, Cch, rmse, acc,
+                                   workspace, workspace_bytes, (hipStream_t)stream, "nsw_weighted_metrics");
+}
+
+extern "C" int nsw_weighted_metrics_unnorm(const void* pred, int pred_dtype, const float* target,
+                                           const float* std_c, const float* mean_c, const double* w,
+                                           int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
+                                           int64_t Cch, double* rmse, double* acc, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  const char* what = "nsw_weighted_metrics_unnorm";
   hipStream_t st = (hipStream_t)stream;
-  double* partial = (double*)workspace;
-  const bool vec4 = (W % 4 == 0) && ((uintptr_t)pred % 16 == 0) && ((uintptr_t)target % 16 == 0);
-  dim3 grid((unsigned)(P * nchunk));
-  if (w_cols == 1 || W == 1)
-    launch_partial<false>(vec4, clim != nullptr, grid, st, pred, target, w, clim, (int)H, (int)W, (int)Cch, rpc, nchunk, partial);
-  else
-    launch_partial<true>(vec4, clim != nullptr, grid, st, pred, target, w, clim, (int)H, (int)W, (int)Cch, rpc, nchunk, partial);
-  int rc = check_launch(what);
-  if (rc) return rc;
-  hipLaunchKernelGGL(wsum_final_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, st, partial, P,
-                     nchunk, (double)(H * W), clim != nullptr, rmse, acc);
-  return check_launch(what);
+  if (pred_dtype == NSW_DTYPE_F32)
+    return run_metrics<float, true>((const float*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W, Cch,
+                                    rmse, acc, workspace, workspace_bytes, st, what);
+  if (pred_dtype == NSW_DTYPE_BF16)
+    return run_metrics<bf16, true>((const bf16*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W, Cch,
+                                   rmse, acc, workspace, workspace_bytes, st, what);
+  return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, pred_dtype);
 }

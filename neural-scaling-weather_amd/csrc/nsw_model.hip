@@ -1,0 +1,230 @@
+// Model-level layout kernels around the Swin blocks: the patch matrix of the
+// stride-p patch convolution (PatchEmbedLayer, models/layer_helpers.py:120-172,
+// used by SwinTransformer.prepare_tokens, models/swin.py:269-284) and the
+// head's unpatchify (SwinTransformer.forward_head, models/swin.py:286-299).
+// Both are pure index permutations, HBM-bound, done as a transpose through
+// LDS: a workgroup owns R consecutive patch rows, reads the image side along
+// its contiguous rows (p consecutive pixels per patch row segment, adjacent
+// patches adjacent in memory) and the patch-matrix side as whole contiguous
+// rows with 16-byte vectors.
+//
+// Patch matrix: row (b, t, i, j) of [B*T*h*w, Kp], column k = (c*p + u)*p + v
+// (the flattening order of a Conv2d weight [E, C, p, p]) holds
+// src[b, t, c, i*p + u, j*p + v]; columns C*p*p .. Kp-1 are zero (Kp pads K to
+// the GEMM's k granularity).  Channels c < C_x come from the frames of x, the
+// others from the invariant fields (the preprocessor's channel concatenation,
+// utils/data_utils.py:185-189, without materialising it), and frame t is read
+// from slot (t + frame0) mod T of x, so that a ring buffer stands in for the
+// inference loop's roll of the input window (utils/inferencer.py:448-449).
+//
+// Unpatchify: out[b, c, i*p + u, j*p + v] = y[(b, i, j), (u*p + v)*C_out + c].
+#include "nsw_common.h"
+
+namespace nsw {
+
+constexpr int MODEL_LDS = 64 * 1024;   // dynamic LDS per workgroup
+
+template <typename T> struct VecOf;
+template <> struct VecOf<bf16> { using V = bf16x8; };
+template <> struct VecOf<float> { using V = f32x4; };
+
+template <typename TX, typename TO>
+__global__ __launch_bounds__(256) void im2col_kernel(const TX* __restrict__ x, const TX* __restrict__ inv,
+                                                     int Cx, int Cinv, int T, int H, int W, int p,
+                                                     int frame0, int Kp, int64_t M, int R,
+                                                     TO* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  TO* tile = reinterpret_cast<TO*>(smem);
+  constexpr int V = 16 / sizeof(TO);
+  const int KS = Kp + V;                        // LDS row stride (16 B of padding)
+  const int64_t m0 = (int64_t)blockIdx.x * R;
+  const int rows = (int)min((int64_t)R, M - m0);
+  const int h = H / p, w = W / p, pp = p * p;
+  const int C = Cx + Cinv, Kc = C * pp;
+  const int64_t HW = (int64_t)H * W;
+  const int tid = threadIdx.x;
+
+  // per-row source offsets (channel 0, pixel (i*p, j*p)) of x and of inv
+  __shared__ int64_t xbase[256];
+  __shared__ int ibase[256];
+  for (int r = tid; r < rows; r += 256) {
+    const int64_t m = m0 + r;
+    const int j = (int)(m % w);
+    const int64_t q = m / w;
+    const int i = (int)(q % h);
+    const int64_t bt = q / h;
+    const int t = (int)(bt % T);
+    const int64_t b = bt / T;
+    int ts = t + frame0;
+    if (ts >= T) ts -= T;
+    const int pix = (i * p) * W + j * p;
+    xbase[r] = ((b * T + ts) * Cx) * HW + pix;
+    ibase[r] = pix;
+  }
+  __syncthreads();
+
+  // gather: lanes (r, v), one (c, u) pair per lane group and iteration
+  const int lanes = rows * p;
+  const int groups = 256 / (R * p);
+  const int lane = tid % (R * p), grp = tid / (R * p);
+  if (lane < lanes && grp < groups) {
+    const int r = lane / p, v = lane - r * p;
+    TO* trow = tile + r * KS + v;
+    for (int cu = grp; cu < C * p; cu += groups) {
+      const int c = cu / p, u = cu - c * p;
+      float val;
+      if (c < Cx) val = to_f32(x[xbase[r] + c * HW + (int64_t)u * W + v]);
+      else val = to_f32(inv[(int64_t)(c - Cx) * HW + ibase[r] + u * W + v]);
+      trow[cu * p] = from_f32<TO>(val);
+    }
+  }
+  // zero padding columns
+  const int padw = Kp - Kc;
+  for (int e = tid; e < rows * padw; e += 256) {
+    const int r = e / padw;
+    tile[r * KS + Kc + (e - r * padw)] = from_f32<TO>(0.f);
+  }
+  __syncthreads();
+
+  // write whole rows (contiguous in out) with 16-byte vectors
+  using Vt = typename VecOf<TO>::V;
+  const int vpr = Kp / V;
+  Vt* orow = reinterpret_cast<Vt*>(out + m0 * Kp);
+  for (int e = tid; e < rows * vpr; e += 256) {
+    const int r = e / vpr, cc = e - r * vpr;
+    orow[e] = *reinterpret_cast<const Vt*>(tile + r * KS + cc * V);
+  }
+}
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void unpatchify_kernel(const TI* __restrict__ y, int Co, int H, int W, int p,
+                                                         int64_t out_bstride, int64_t M, int R,
+                                                         TO* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  TI* tile = reinterpret_cast<TI*>(smem);
+  constexpr int V = 16 / sizeof(TI);
+  const int N = p * p * Co;
+  const int NS = N + V;
+  const int64_t m0 = (int64_t)blockIdx.x * R;
+  const int rows = (int)min((int64_t)R, M - m0);
+  const int h = H / p, w = W / p;
+  const int64_t HW = (int64_t)H * W;
+  const int tid = threadIdx.x;
+
+  __shared__ int64_t obase[256];
+  for (int r = tid; r < rows; r += 256) {
+    const int64_t m = m0 + r;
+    const int j = (int)(m % w);
+    const int64_t q = m / w;
+    const int i = (int)(q % h);
+    const int64_t b = q / h;
+    obase[r] = b * out_bstride + (int64_t)(i * p) * W + j * p;
+  }
+  // load whole rows (contiguous in y) with 16-byte vectors
+  using Vt = typename VecOf<TI>::V;
+  const int vpr = N / V;
+  const Vt* yrow = reinterpret_cast<const Vt*>(y + m0 * N);
+  for (int e = tid; e < rows * vpr; e += 256) {
+    const int r = e / vpr, cc = e - r * vpr;
+    *reinterpret_cast<Vt*>(tile + r * NS + cc * V) = yrow[e];
+  }
+  __syncthreads();
+
+  // scatter: lanes (r, v) write p consecutive pixels of adjacent patches
+  const int lanes = rows * p;
+  const int groups = 256 / (R * p);
+  const int lane = tid % (R * p), grp = tid / (R * p);
+  if (lane < lanes && grp < groups) {
+    const int r = lane / p, v = lane - r * p;
+    const TI* trow = tile + r * NS + v * Co;
+    for (int cu = grp; cu < Co * p; cu += groups) {
+      const int c = cu / p, u = cu - c * p;
+      out[obase[r] + c * HW + (int64_t)u * W + v] = from_f32<TO>(to_f32(trow[u * p * Co + c]));
+    }
+  }
+}
+
+// Rows per workgroup: at most 256 / p (one lane per pixel of a patch row
+// segment) and at most MODEL_LDS of tile.
+static int rows_per_wg(int p, int row_bytes) {
+  int r = 256 / p;
+  const int lim = MODEL_LDS / row_bytes;
+  if (lim < r) r = lim;
+  return r < 1 ? 1 : r;
+}
+
+}  // namespace nsw
+
+using namespace nsw;
+
+extern "C" int nsw_patch_im2col(const void* x, const void* inv, int64_t B, int64_t T, int64_t C_x,
+                                int64_t C_inv, int64_t H, int64_t W, int64_t p, int64_t frame0,
+                                int64_t Kp, void* out, int x_dtype, int out_dtype, void* stream) {
+  const char* what = "nsw_patch_im2col";
+  NSW_CHECK_ARG(B > 0 && T > 0 && C_x > 0 && C_inv >= 0 && H > 0 && W > 0 && p > 0,
+                "%s: B, T, C_x, H, W, p must be positive (C_inv >= 0)", what);
+  NSW_CHECK_ARG(p <= 16 && H % p == 0 && W % p == 0, "%s: H=%lld, W=%lld not divisible by p=%lld (p <= 16)",
+                what, (long long)H, (long long)W, (long long)p);
+  NSW_CHECK_ARG(C_inv == 0 || inv != nullptr, "%s: invariant channels without data", what);
+  NSW_CHECK_ARG(frame0 >= 0 && frame0 < T, "%s: frame0 must lie in [0, T)", what);
+  const int64_t Kc = (C_x + C_inv) * p * p;
+  const int V = out_dtype == NSW_DTYPE_BF16 ? 8 : 4;
+  NSW_CHECK_ARG(Kp >= Kc && Kp % V == 0, "%s: Kp=%lld must be >= C*p*p=%lld and a multiple of %d", what,
+                (long long)Kp, (long long)Kc, V);
+  NSW_CHECK_ARG(((uintptr_t)out % 16) == 0, "%s: out must be 16-byte aligned", what);
+  NSW_CHECK_ARG(B * T * C_x * H * W < (1LL << 40) && H * W < (1LL << 31), "%s: too large", what);
+  const int64_t M = B * T * (H / p) * (W / p);
+  const size_t es = dtype_size(out_dtype);
+  const int row_bytes = (int)((Kp + V) * es);
+  NSW_CHECK_ARG(row_bytes <= MODEL_LDS, "%s: Kp=%lld too large for one LDS row", what, (long long)Kp);
+  const int R = rows_per_wg((int)p, row_bytes);
+  const int64_t grid = (M + R - 1) / R;
+  NSW_CHECK_ARG(grid < (1LL << 31), "%s: too many rows", what);
+  hipStream_t st = (hipStream_t)stream;
+  const size_t shm = (size_t)R * row_bytes;
+  const dim3 g((unsigned)grid), blk(256);
+#define NSW_IM2COL(TX, TO)                                                                              \
+  hipLaunchKernelGGL((im2col_kernel<TX, TO>), g, blk, shm, st, (const TX*)x, (const TX*)inv, (int)C_x, \
+                     (int)C_inv, (int)T, (int)H, (int)W, (int)p, (int)frame0, (int)Kp, M, R, (TO*)out)
+  if (x_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_BF16) NSW_IM2COL(float, bf16);
+  else if (x_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_F32) NSW_IM2COL(float, float);
+  else if (x_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_BF16) NSW_IM2COL(bf16, bf16);
+  else if (x_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_F32) NSW_IM2COL(bf16, float);
+  else return set_error(NSW_ERR_INVALID, "%s: unknown dtype pair %d -> %d", what, x_dtype, out_dtype);
+#undef NSW_IM2COL
+  return check_launch(what);
+}
+
+extern "C" int nsw_unpatchify(const void* y, void* out, int64_t B, int64_t C_out, int64_t H, int64_t W,
+                              int64_t p, int64_t out_bstride, int in_dtype, int out_dtype, void* stream) {
+  const char* what = "nsw_unpatchify";
+  NSW_CHECK_ARG(B > 0 && C_out > 0 && H > 0 && W > 0 && p > 0, "%s: B, C_out, H, W, p must be positive", what);
+  NSW_CHECK_ARG(p <= 16 && H % p == 0 && W % p == 0, "%s: H=%lld, W=%lld not divisible by p=%lld (p <= 16)",
+                what, (long long)H, (long long)W, (long long)p);
+  NSW_CHECK_ARG(out_bstride >= C_out * H * W, "%s: out_bstride smaller than one sample", what);
+  const int64_t N = p * p * C_out;
+  const int V = in_dtype == NSW_DTYPE_BF16 ? 8 : 4;
+  NSW_CHECK_ARG(N % V == 0, "%s: p*p*C_out=%lld must be a multiple of %d", what, (long long)N, V);
+  NSW_CHECK_ARG(((uintptr_t)y % 16) == 0, "%s: y must be 16-byte aligned", what);
+  NSW_CHECK_ARG(B * out_bstride < (1LL << 40), "%s: too large", what);
+  const int64_t M = B * (H / p) * (W / p);
+  const size_t es = dtype_size(in_dtype);
+  const int row_bytes = (int)((N + V) * es);
+  NSW_CHECK_ARG(row_bytes <= MODEL_LDS, "%s: p*p*C_out=%lld too large for one LDS row", what, (long long)N);
+  const int R = rows_per_wg((int)p, row_bytes);
+  const int64_t grid = (M + R - 1) / R;
+  NSW_CHECK_ARG(grid < (1LL << 31), "%s: too many rows", what);
+  hipStream_t st = (hipStream_t)stream;
+  const size_t shm = (size_t)R * row_bytes;
+  const dim3 g((unsigned)grid), blk(256);
+#define NSW_UNPATCH(TI, TO)                                                                           \
+  hipLaunchKernelGGL((unpatchify_kernel<TI, TO>), g, blk, shm, st, (const TI*)y, (int)C_out, (int)H, \
+                     (int)W, (int)p, out_bstride, M, R, (TO*)out)
+  if (in_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_BF16) NSW_UNPATCH(bf16, bf16);
+  else if (in_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_F32) NSW_UNPATCH(bf16, float);
+  else if (in_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_F32) NSW_UNPATCH(float, float);
+  else if (in_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_BF16) NSW_UNPATCH(float, bf16);
+  else return set_error(NSW_ERR_INVALID, "%s: unknown dtype pair %d -> %d", what, in_dtype, out_dtype);
+#undef NSW_UNPATCH
+  return check_launch(what);
+}

@@ -69,6 +69,11 @@ SIGNATURES = {
     "nsw_weighted_metrics_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "nsw_weighted_metrics": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
                                     ctypes.c_size_t, _vp]),
+    "nsw_weighted_metrics_unnorm": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
+                                           _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "nsw_patch_im2col": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _int,
+                                _int, _vp]),
+    "nsw_unpatchify": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
 }
 
 _lib = None

@@ -170,10 +170,12 @@ def rmsnorm_roll_partition(x: torch.Tensor, weight: torch.Tensor, window_size, s
 # -------------------------------------------------------------------- GEMM ---
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
-           residual: Optional[torch.Tensor] = None, epilogue: Optional[int] = None) -> torch.Tensor:
-    """y = epi(x . weight^T): F.linear with an optional fused bias / GELU / residual."""
-    dev = _dev(x, weight, bias, residual)
-    _same_dtype(x, weight, bias, residual)
+           residual: Optional[torch.Tensor] = None, epilogue: Optional[int] = None,
+           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = epi(x . weight^T): F.linear with an optional fused bias / GELU / residual.
+    ``out`` (contiguous, x.shape[:-1] + (N,), x's dtype) receives y if given."""
+    dev = _dev(x, weight, bias, residual, out)
+    _same_dtype(x, weight, bias, residual, out)
     K = x.shape[-1]
     N, Kw = weight.shape
     if Kw != K:
@@ -182,7 +184,12 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     if epilogue is None:
         epilogue = _lib.NSW_EPI_NONE if bias is None else (
             _lib.NSW_EPI_BIAS if residual is None else _lib.NSW_EPI_BIAS_RESIDUAL)
-    y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=dev)
+    if out is not None:
+        if out.numel() != M * N:
+            raise ValueError(f"linear: out has {out.numel()} elements, expected {M * N}")
+        y = out.view(x.shape[:-1] + (N,))
+    else:
+        y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=dev)
     if residual is not None and residual.shape != y.shape:
         raise ValueError(f"residual shape {tuple(residual.shape)} != output {tuple(y.shape)}")
     check(lib().nsw_linear(x.data_ptr(), weight.data_ptr(), _p(bias), _p(residual), y.data_ptr(), M, N, K,
@@ -325,5 +332,99 @@ def weighted_metrics(pred: torch.Tensor, target: torch.Tensor, weights: torch.Te
                                      H, W, C,
                                      rmse.data_ptr(), _p(acc), ws.data_ptr(), ws.numel(), _stream(dev)),
           "weighted_metrics")
+    rmse = rmse.view(B, T, C)
+    return rmse, (acc.view(B, T, C) if acc is not None else None)
+
+
+# ------------------------------------------------------------ model layout ---
+
+def k_granule(dtype: torch.dtype) -> int:
+    """GEMM k granularity of nsw_linear: 64 (bf16) / 32 (f32) elements."""
+    return 64 if dtype == torch.bfloat16 else 32
+
+
+def patch_im2col(x: torch.Tensor, p: int, Kp: int, dtype: torch.dtype,
+                 invariants: Optional[torch.Tensor] = None, frame0: int = 0) -> torch.Tensor:
+    """Patch matrix of the stride-p patch convolution: x [B, T, C_x, H, W]
+    (+ invariants [C_inv, H, W] as extra channels; frame t read from slot
+    (t + frame0) mod T) -> [B*T*(H/p)*(W/p), Kp] in ``dtype``."""
+    if x.dim() != 5:
+        raise ValueError("patch_im2col: x must be [B, T, C, H, W]")
+    B, T, Cx, H, W = x.shape
+    if invariants is not None:
+        if invariants.dtype != x.dtype:
+            raise TypeError("patch_im2col: invariants must have x's dtype")
+        if invariants.dim() != 3 or tuple(invariants.shape[1:]) != (H, W):
+            raise ValueError("patch_im2col: invariants must be [C_inv, H, W]")
+    dev = _dev(x, invariants)
+    Cinv = 0 if invariants is None else invariants.shape[0]
+    M = B * T * (H // p) * (W // p)
+    out = torch.empty(M, Kp, dtype=dtype, device=dev)
+    check(lib().nsw_patch_im2col(x.data_ptr(), _p(invariants), B, T, Cx, Cinv, H, W, p, int(frame0), Kp,
+                                 out.data_ptr(), dtype_code(x), _DTYPES[dtype], _stream(dev)), "patch_im2col")
+    return out
+
+
+def unpatchify(y: torch.Tensor, B: int, C_out: int, H: int, W: int, p: int,
+               dtype: Optional[torch.dtype] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Head layout: y [B*(H/p)*(W/p), p*p*C_out] -> [B, 1, C_out, H, W].  With
+    ``out`` (a [B, 1, C_out, H, W] tensor whose frames are contiguous, e.g.
+    one slot of a [B, T, C, H, W] ring buffer) the result is written there in
+    out's dtype."""
+    if out is not None:
+        if tuple(out.shape) != (B, 1, C_out, H, W):
+            raise ValueError(f"unpatchify: out must be [{B}, 1, {C_out}, {H}, {W}]")
+        if out.stride()[2:] != (H * W, W, 1) or out.stride(0) < C_out * H * W:
+            raise ValueError("unpatchify: every frame of out must be contiguous")
+        if not out.is_cuda:
+            raise RuntimeError("libnsw ops run on the GPU only")
+        bstride = out.stride(0)
+        dst = out
+    else:
+        dst = torch.empty(B, 1, C_out, H, W, dtype=dtype or y.dtype, device=y.device)
+        bstride = C_out * H * W
+    dev = _dev(y)
+    if dst.device != dev:
+        raise RuntimeError("libnsw op arguments are on different devices")
+    check(lib().nsw_unpatchify(y.data_ptr(), dst.data_ptr(), B, C_out, H, W, p, bstride, dtype_code(y),
+                               dtype_code(dst), _stream(dev)), "unpatchify")
+    return dst
+
+
+def weighted_metrics_unnorm(pred: torch.Tensor, target: torch.Tensor, std: torch.Tensor, mean: torch.Tensor,
+                            weights: torch.Tensor, clim: Optional[torch.Tensor] = None):
+    """Weighted RMSE (and ACC with ``clim``) of pred * std + mean against
+    target * std + mean, per (b, t, c), float64 [B, T, C].  pred fp32 or
+    bf16, target fp32, std / mean per channel."""
+    if pred.shape != target.shape or pred.dim() != 5:
+        raise ValueError("pred and target must be [B, T, C, H, W] of the same shape")
+    if target.dtype != torch.float32:
+        raise TypeError("target must be float32")
+    B, T, C, H, W = pred.shape
+    dev = _dev(pred, target)
+    w = weights.to(device=dev, dtype=torch.float64).contiguous()
+    if w.numel() == H:
+        w_cols = 1
+    elif w.numel() == H * W and (w.dim() < 2 or tuple(w.shape[-2:]) == (H, W)):
+        w_cols = W
+    else:
+        raise ValueError(f"weights of shape {tuple(weights.shape)} do not match a {H}x{W} field")
+    sc = std.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+    of = mean.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+    if sc.numel() != C or of.numel() != C:
+        raise ValueError("std and mean must have one value per channel")
+    if clim is not None:
+        clim = clim.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+        if clim.numel() != C:
+            raise ValueError("climatology must have one value per channel")
+    P = B * T * C
+    rmse = torch.empty(P, dtype=torch.float64, device=dev)
+    acc = torch.empty(P, dtype=torch.float64, device=dev) if clim is not None else None
+    nbytes = lib().nsw_weighted_metrics_workspace_size(P, H, W)
+    ws = workspace(max(nbytes, 8), dev)
+    check(lib().nsw_weighted_metrics_unnorm(pred.data_ptr(), dtype_code(pred), target.data_ptr(), sc.data_ptr(),
+                                            of.data_ptr(), w.data_ptr(), w_cols, _p(clim), P, H, W, C,
+                                            rmse.data_ptr(), _p(acc), ws.data_ptr(), ws.numel(), _stream(dev)),
+          "weighted_metrics_unnorm")
     rmse = rmse.view(B, T, C)
     return rmse, (acc.view(B, T, C) if acc is not None else None)

@@ -1,0 +1,314 @@
+"""SwinTransformer and its patch-embedding layers (models/swin.py:44-323,
+models/layer_helpers.py:120-172), with the reference's constructor
+signatures, attribute names and state-dict keys, running libnsw kernels.
+
+Forward path on the GPU (models/swin.py:301-323):
+  prepare_tokens  patch matrix of the input (nsw_patch_im2col) -> one GEMM
+                  with the conv bias and the positional embedding fused in its
+                  epilogue (bias + residual) -> tokens [B, T, h, w, E];
+                  the coordinate embedding is the same patch GEMM over the
+                  constant coordinate fields, computed once and cached until
+                  its weights change.
+  blocks          nsw.Block (the fused shifted-window block).
+  forward_head    GEMM E -> C_out*p*p (no bias) -> nsw_unpatchify.  forward()
+                  applies the head to the last frame only, which equals the
+                  reference's all-frame head followed by ``x[:, -1:]`` because
+                  the head is per token.
+The optional big skip convolution (``use_big_skip_conv=True``, off by
+default and in every configuration of the reference's experiments) is not
+implemented and raises.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import nn
+
+from . import ops
+from .layer_helpers import LinearLayer, trunc_normal_
+from .swin_helpers import Block as BlockDefault
+
+_EMBED_META = {"sharded": [], "shared": ["tp-sp1-sp2"], "reduce": ["sp1-sp2"]}
+
+
+class Conv2DLayer(nn.Module):
+    """``Conv2DLayer`` (models/layer_helpers.py:152-172): holds ``conv`` (an
+    nn.Conv2d, for the parameter names and init); stride = kernel_size is the
+    only case the model uses and the only one the forward runs."""
+
+    def __init__(self, in_chans, out_chans, kernel_size, stride=1, bias=True, comm_metadata=None):
+        super().__init__()
+        self.conv = nn.Conv2d(in_chans, out_chans, kernel_size=kernel_size, stride=stride, bias=bias)
+        meta = comm_metadata or dict(_EMBED_META)
+        self.conv.weight.comm_metadata = meta
+        if bias:
+            self.conv.bias.comm_metadata = meta
+
+    def forward(self, x):
+        raise NotImplementedError("Conv2DLayer runs inside PatchEmbedLayer (stride = kernel size) only")
+
+
+class PatchEmbedLayer(nn.Module):
+    """``PatchEmbedLayer`` (models/layer_helpers.py:120-150): Conv2d with
+    kernel = stride = patch_size as a patch-matrix GEMM."""
+
+    def __init__(self, patch_size=16, in_chans=3, embed_dim=768, sp1_shapes=None, sp2_shapes=None,
+                 comm_metadata=None):
+        super().__init__()
+        if sp1_shapes is None or sp2_shapes is None:
+            raise ValueError("PatchEmbedLayer needs the image extent (sp1_shapes=[H], sp2_shapes=[W])")
+        if len(sp1_shapes) != 1 or len(sp2_shapes) != 1:
+            raise NotImplementedError("libnsw runs the single-GPU (unsharded) model")
+        self.proj = Conv2DLayer(in_chans, embed_dim, kernel_size=patch_size, stride=patch_size,
+                                comm_metadata=comm_metadata)
+        self.patch_size = patch_size
+        self.in_chans = in_chans
+        self.embed_dim = embed_dim
+        self.sp1_patch_shapes = [s // patch_size for s in sp1_shapes]
+        self.h = self.sp1_patch_shapes[0]
+        self.sp2_patch_shapes = [s // patch_size for s in sp2_shapes]
+        self.w = self.sp2_patch_shapes[0]
+        self.num_patches = self.h * self.w
+        self._pack_key = None
+        self._pack = None
+
+    def packed(self):
+        """Weight as a [E, Kp] GEMM operand (rows of the Conv2d weight in
+        (c, u, v) order, zero columns up to the GEMM k granularity), cached
+        until the parameters change."""
+        w, b = self.proj.conv.weight, self.proj.conv.bias
+        key = (w.data_ptr(), w._version, w.dtype, w.device,
+               None if b is None else (b.data_ptr(), b._version))
+        if self._pack_key != key:
+            E = w.shape[0]
+            K = w[0].numel()
+            g = ops.k_granule(w.dtype)
+            Kp = (K + g - 1) // g * g
+            wp = torch.zeros(E, Kp, dtype=w.dtype, device=w.device)
+            with torch.no_grad():
+                wp[:, :K].copy_(w.detach().reshape(E, K))
+            self._pack = (wp, None if b is None else b.detach().contiguous(), Kp)
+            self._pack_key = key
+        return self._pack
+
+    def tokens(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
+               invariants: Optional[torch.Tensor] = None, frame0: int = 0) -> torch.Tensor:
+        """[B, T, C, H, W] -> conv output in token layout [B, T, h, w, E],
+        plus ``residual`` [B*T*h*w, E] if given."""
+        B, T, C, H, W = x.shape
+        p = self.patch_size
+        if H != self.h * p or W != self.w * p:
+            raise ValueError(f"input extent {(H, W)} does not match the layer's {(self.h * p, self.w * p)}")
+        wp, b, Kp = self.packed()
+        pm = ops.patch_im2col(x.contiguous(), p, Kp, wp.dtype, invariants=invariants, frame0=frame0)
+        if b is None:
+            if residual is not None:
+                raise NotImplementedError("a residual without a conv bias is not fused")
+            y = ops.linear(pm, wp)
+        else:
+            y = ops.linear(pm, wp, b, residual=residual)
+        return y.view(B, T, H // p, W // p, self.embed_dim)
+
+    def forward(self, x):
+        """Conv2d semantics: [N, C, H, W] -> [N, E, H/p, W/p]."""
+        return self.tokens(x.unsqueeze(1))[:, 0].permute(0, 3, 1, 2)
+
+
+class SwinTransformer(nn.Module):
+    """``SwinTransformer`` (models/swin.py:44-323) for one GPU."""
+
+    @classmethod
+    def instantiate_from_cfg(cls, cfg, domain_metadata):
+        """models/swin.py:61-85 (cfg with attribute access: cfg.model.*,
+        cfg.train.temporal_context_window, cfg.data.invariants,
+        cfg.parallelism.use_transformer_engine)."""
+        ws = cfg.model.window_size
+        window_size = tuple(ws) if isinstance(ws, (list, tuple)) else (ws, ws)
+        invariants = getattr(cfg.data, "invariants", None)
+        extra_inputs = len(invariants) if invariants else 0
+        return cls(
+            patch_size=cfg.model.patch_size,
+            window_size=window_size,
+            depth=cfg.model.depth,
+            num_heads=cfg.model.num_heads,
+            temporal_context_window_size=cfg.train.temporal_context_window,
+            in_chans=domain_metadata["n_channels"] + extra_inputs,
+            out_chans=domain_metadata["n_channels"],
+            embed_dim=cfg.model.embed_dim,
+            mlp_ratio=cfg.model.mlp_ratio,
+            drop_rate=cfg.model.dropout,
+            coord_pos_embed=getattr(cfg.model, "coord_pos_embed", True),
+            use_transformer_engine=getattr(getattr(cfg, "parallelism", None), "use_transformer_engine", True),
+            domain_metadata=domain_metadata,
+        )
+
+    def __init__(self, temporal_context_window_size=1, window_size=(9, 9), patch_size=16, in_chans=3,
+                 out_chans=3, embed_dim=768, depth=12, num_heads=12, mlp_ratio=4.0, drop_rate=0.0,
+                 coord_pos_embed=True, domain_metadata=None, use_transformer_engine=True,
+                 use_big_skip_conv=False, **kwargs):
+        super().__init__()
+        if use_big_skip_conv:
+            raise NotImplementedError("use_big_skip_conv=True is not implemented in libnsw")
+        if domain_metadata is None:
+            raise ValueError("data loader must provide domain metadata")
+        self.num_features = self.embed_dim = embed_dim
+        self.patch_size = patch_size
+        self.temporal_context_window_size = temporal_context_window_size
+        self.window_size = tuple(window_size)
+        self.in_chans = in_chans
+        self.out_chans = out_chans
+        self.drop_rate = drop_rate
+        self.coord_pos_embed = coord_pos_embed
+        self.domain_metadata = domain_metadata
+        self.use_transformer_engine = use_transformer_engine
+        self.use_big_skip_conv = use_big_skip_conv
+        sp1, sp2 = domain_metadata["sp_shapes"]
+
+        self.patch_embed = PatchEmbedLayer(patch_size=patch_size, in_chans=in_chans, embed_dim=embed_dim,
+                                           sp1_shapes=sp1, sp2_shapes=sp2, comm_metadata=dict(_EMBED_META))
+        if coord_pos_embed:
+            self._init_coords()
+            self.pos_embed = PatchEmbedLayer(patch_size=patch_size, in_chans=self.coords.shape[-1],
+                                             embed_dim=embed_dim, sp1_shapes=sp1, sp2_shapes=sp2,
+                                             comm_metadata=dict(_EMBED_META))
+        else:
+            self.pos_embed = nn.Parameter(torch.zeros(1, temporal_context_window_size, self.patch_embed.h,
+                                                      self.patch_embed.w, embed_dim))
+            trunc_normal_(self.pos_embed, std=0.02)
+            self.pos_embed.comm_metadata = {"sharded": [None, None, "sp1", "sp2", None], "shared": ["tp"],
+                                            "reduce": []}
+
+        self.blocks = nn.ModuleList([
+            BlockDefault(dim=embed_dim, num_heads=num_heads, feat_size=(self.patch_embed.h, self.patch_embed.w),
+                         window_size=self.window_size, temporal_context_window_size=temporal_context_window_size,
+                         shift_size=tuple(0 if (i % 2) == 0 else w // 2 for w in self.window_size),
+                         mlp_ratio=mlp_ratio, drop=drop_rate, sp1_shapes=self.patch_embed.sp1_patch_shapes,
+                         sp2_shapes=self.patch_embed.sp2_patch_shapes)
+            for i in range(depth)])
+        self.out_size = out_chans * patch_size * patch_size
+        self.head = LinearLayer(embed_dim, self.out_size, comm_metadata=dict(_EMBED_META))
+        self.apply(self._init_weights)
+        self._pos_key = None
+        self._pos = None
+
+    def _init_coords(self):
+        """models/swin.py:227-244: coords [T, H, W, 4] = spatial (x, y, z) with
+        t = linspace(0, 1, T) appended (non-persistent buffer)."""
+        T = self.temporal_context_window_size
+        spatial = torch.as_tensor(self.domain_metadata["coords"]).float()
+        H, W, _ = spatial.shape
+        t = torch.linspace(0, 1, T).view(T, 1, 1, 1).expand(-1, H, W, 1)
+        coords = torch.cat([spatial.unsqueeze(0).expand(T, -1, -1, -1), t], dim=-1)
+        self.register_buffer("coords", coords, persistent=False)
+
+    def _init_weights(self, m):
+        """models/swin.py:246-267."""
+        if isinstance(m, (nn.Linear, nn.Conv2d)):
+            trunc_normal_(m.weight, std=0.02)
+            if m.bias is not None:
+                nn.init.constant_(m.bias, 0)
+        elif isinstance(m, nn.LayerNorm):
+            nn.init.constant_(m.bias, 0)
+            nn.init.constant_(m.weight, 1.0)
+        elif isinstance(m, nn.RMSNorm):
+            nn.init.constant_(m.weight, 1.0)
+
+    # ------------------------------------------------------------ embedding --
+    def _pos_tokens(self, B: int, dtype: torch.dtype, device) -> torch.Tensor:
+        """Positional embedding in token layout, repeated over the batch:
+        [B*T*h*w, E] (the GEMM epilogue's residual operand)."""
+        if self.coord_pos_embed:
+            w, b = self.pos_embed.proj.conv.weight, self.pos_embed.proj.conv.bias
+            key = ("coord", w.data_ptr(), w._version, b.data_ptr(), b._version, self.coords.data_ptr(),
+                   self.coords._version, dtype, torch.device(device), B)
+        else:
+            key = ("param", self.pos_embed.data_ptr(), self.pos_embed._version, dtype, torch.device(device), B)
+        if self._pos_key != key:
+            with torch.no_grad():
+                if self.coord_pos_embed:
+                    c = self.coords.to(device=device, dtype=self.pos_embed.proj.conv.weight.dtype)
+                    c = c.permute(0, 3, 1, 2).contiguous().unsqueeze(0)       # [1, T, 4, H, W]
+                    pos = self.pos_embed.tokens(c)                             # [1, T, h, w, E]
+                else:
+                    pos = self.pos_embed.detach()
+                pos = pos.to(device=device, dtype=dtype).expand(B, -1, -1, -1, -1)
+                self._pos = pos.reshape(-1, self.embed_dim).contiguous()
+            self._pos_key = key
+        return self._pos
+
+    def prepare_tokens(self, x: torch.Tensor, invariants: Optional[torch.Tensor] = None,
+                       frame0: int = 0) -> torch.Tensor:
+        """models/swin.py:269-284: [B, T, C, H, W] -> [B, T, h, w, E]."""
+        w = self.patch_embed.proj.conv.weight
+        pos = self._pos_tokens(x.shape[0], w.dtype, w.device)
+        return self.patch_embed.tokens(x, residual=pos, invariants=invariants, frame0=frame0)
+
+    # ----------------------------------------------------------------- head --
+    def forward_head(self, x: torch.Tensor) -> torch.Tensor:
+        """models/swin.py:286-299: [B, T, h, w, E] -> [B, T, C_out, H, W]."""
+        b, t, h, w, c = x.shape
+        p = self.patch_size
+        y = ops.linear(x.contiguous().view(-1, c), self.head.weight)
+        out = ops.unpatchify(y, b * t, self.out_chans, h * p, w * p, p)
+        return out.view(b, t, self.out_chans, h * p, w * p)
+
+    def _head_last(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Head of the last frame only: [B, T, h, w, E] -> [B, 1, C_out, H, W]
+        (into ``out`` when given, in out's dtype)."""
+        b, t, h, w, c = x.shape
+        p = self.patch_size
+        W = self.head.weight
+        y = torch.empty(b * h * w, self.out_size, dtype=x.dtype, device=x.device)
+        for bi in range(b):
+            ops.linear(x[bi, t - 1].view(h * w, c), W, out=y[bi * h * w:(bi + 1) * h * w])
+        return ops.unpatchify(y, b, self.out_chans, h * p, w * p, p, out=out)
+
+    # -------------------------------------------------------------- forward --
+    def forward(self, x: torch.Tensor, invariants: Optional[torch.Tensor] = None, frame0: int = 0,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """models/swin.py:301-323: [B, T, C_in, H, W] -> [B, 1, C_out, H, W].
+
+        Beyond the reference's signature (all optional): ``invariants``
+        [C_inv, H, W] are appended as input channels inside the patch gather,
+        frame t is read from slot (t + frame0) mod T of x, and ``out`` receives
+        the prediction (any float dtype; e.g. a slot of the input ring)."""
+        y = self.prepare_tokens(x, invariants=invariants, frame0=frame0)
+        for blk in self.blocks:
+            y = blk(y)
+        return self._head_last(y, out=out)
+
+
+class TimeStepper(nn.Module):
+    """``TimeStepper`` (models/helpers.py:9-37): autoregressive steps with the
+    invariant channels re-appended to every prediction."""
+
+    def __init__(self, cfg, model_handle):
+        super().__init__()
+        self.model = model_handle
+        self.num_rollout_steps = cfg.train.num_rollout_steps
+        invariants = getattr(cfg.data, "invariants", None)
+        self.num_invariants = len(invariants) if invariants else 0
+
+    def forward(self, inp):
+        result = []
+        inpt = inp
+        c_in = inp.shape[2]
+        for step in range(self.num_rollout_steps):
+            pred = self.model(inpt)
+            c_out = pred.shape[2]
+            result.append(pred)
+            n_invariants = c_in - c_out
+            assert n_invariants == self.num_invariants, "number of invariants does not match"
+            if n_invariants > 0:
+                inpt = torch.cat([pred.to(inp.dtype), inp[:, :, c_in - n_invariants:]], dim=2)
+            else:
+                inpt = pred
+        return torch.cat(result, dim=1)
+
+
+def get_model(cfg, domain_metadata=None):
+    """models/helpers.py:40-50."""
+    if cfg.model.arch != "swin":
+        raise NotImplementedError(f"model type {cfg.model.arch} not implemented")
+    return TimeStepper(cfg, SwinTransformer.instantiate_from_cfg(cfg, domain_metadata=domain_metadata))
