@@ -9,6 +9,16 @@ tokens/s over K timed steps (inputs resident in HBM), the roofline of the
 dominant kernel from HIP events on the launch stream, the per-kernel
 breakdown, and a CPU baseline (the fp32 oracle on the host cores, on a
 bounded sample of the same workload).  One GPU only.
+
+Unless --no-model is given the line also carries
+  "forecast": config 3, one SwinTransformer forward (p4, e1024, depth 16,
+              16 heads, window 9x18, 70 channels, 720x1440, bf16) = ms per
+              forecast step, split into embedding / blocks / head;
+  "rollout":  config 5, 8 autoregressive steps of the config-3 model with
+              per-step latitude-weighted RMSE and ACC (nsw.Rollout), bf16
+              against the same weights in fp32: per-step drift.
+Inputs there are seeded Gaussian-filtered, per-channel standardised fields
+(sigma = 8 px), standing in for ERA5.
 """
 from __future__ import annotations
 
@@ -65,6 +75,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-model", action="store_true", help="skip the config-3 forecast and config-5 rollout")
+    ap.add_argument("--model-steps", type=int, default=10, help="timed forecast steps (config 3)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (5 launches): the reference kernel whose "
@@ -203,10 +215,122 @@ def main():
         "kernels": kern,
     }
 
+    # ------------------------------------------------- config 3 / config 5
+    if not args.no_model:
+        del y, y2, qkv, o, h1, hn, u, xw
+        torch.cuda.empty_cache()
+        out["forecast"], out["rollout"] = model_sections(dev, args.model_steps, args.warmup)
+
     # ----------------------------------------------------------- CPU baseline
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, args.cpu_seconds)
     print(json.dumps(out), flush=True)
+
+
+def smooth_fields(shape, sigma, seed, dev):
+    """Seeded N(0, 1) noise [..., H, W] convolved with a periodic Gaussian of
+    `sigma` pixels (FFT) and standardised per leading index, on the GPU."""
+    import math
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+    H, W = shape[-2], shape[-1]
+    ky = torch.fft.fftfreq(H, device=dev).view(H, 1)
+    kx = torch.fft.rfftfreq(W, device=dev).view(1, -1)
+    filt = torch.exp(-2.0 * (math.pi * sigma) ** 2 * (ky ** 2 + kx ** 2))
+    flat = x.view(-1, H, W)
+    for i in range(flat.shape[0]):          # one plane at a time: bounded FFT workspace
+        y = torch.fft.irfft2(torch.fft.rfft2(flat[i]) * filt, s=(H, W))
+        flat[i] = (y - y.mean()) / y.std()
+    return x
+
+
+def model_sections(dev, steps, warmup):
+    """Config 3 (one forecast step of the d16 model) and config 5 (8-step
+    rollout, bf16 vs fp32)."""
+    import numpy as np
+    import torch
+    import nsw
+    C, H, W, p, E, depth, heads, ws, T = 70, 720, 1440, 4, 1024, 16, 16, (9, 18), 1
+    lat = nsw.misc_utils.era5_latitudes(H)
+    lon = nsw.misc_utils.era5_longitudes(W)
+    meta = {"coords": nsw.get_spatial_coords((lat, lon)).float(), "sp_shapes": [[H], [W]], "n_channels": C}
+    torch.manual_seed(3001)
+    model = nsw.SwinTransformer(temporal_context_window_size=T, window_size=ws, patch_size=p, in_chans=C,
+                                out_chans=C, embed_dim=E, depth=depth, num_heads=heads, coord_pos_embed=True,
+                                domain_metadata=meta).to(device=dev, dtype=torch.bfloat16).eval()
+    x = smooth_fields((1, T, C, H, W), 8.0, 3002, dev)
+    tokens = (H // p) * (W // p)
+    fl = block_flops(1, T, H // p, W // p, E, heads, ws)
+    step_flops = depth * sum(fl.values()) + 2 * tokens * (C * p * p) * E * 2   # blocks + embed + head GEMMs
+    stream = torch.cuda.current_stream(dev)
+    with torch.inference_mode():
+        for _ in range(warmup):
+            model(x)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            yb = model(x)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        # stage split
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record(stream)
+        tok = model.prepare_tokens(x)
+        ev[1].record(stream)
+        for blk in model.blocks:
+            tok = blk(tok)
+        ev[2].record(stream)
+        model._head_last(tok)
+        ev[3].record(stream)
+        torch.cuda.synchronize()
+        if not torch.isfinite(yb.float()).all():
+            raise RuntimeError("non-finite forecast")
+    forecast = {
+        "workload": "config 3: SwinTransformer fwd, [1,1,70,720,1440] -> [1,1,70,720,1440], p4 e1024 depth 16, "
+                    "16 heads, window 9x18, alternating shift 0 / 4x9, coordinate pos-embed, bf16",
+        "ms_per_step": round(ms, 3), "steps": steps, "tflop_per_step": round(step_flops / 1e12, 3),
+        "tflops_achieved": round(step_flops / (ms * 1e-3) / 1e12, 1),
+        "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+        "embed_ms": round(ev[0].elapsed_time(ev[1]), 3), "blocks_ms": round(ev[1].elapsed_time(ev[2]), 3),
+        "head_ms": round(ev[2].elapsed_time(ev[3]), 3),
+    }
+    del tok, yb
+
+    # config 5: rollout, bf16 and fp32 copies of the same weights
+    S = 8
+    g = torch.Generator().manual_seed(3003)
+    mean = torch.randn(C, generator=g) * 10.0
+    std = torch.rand(C, generator=g) * 1.5 + 0.5
+    clim = mean + std * torch.randn(C, generator=g) * 0.01
+    w = nsw.build_spherical_area_weights(lat)[:, None]
+    targets = smooth_fields((S, C, H, W), 8.0, 3004, dev)
+    res = {}
+    for name, dt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
+        m = model if dt == torch.bfloat16 else model.float()
+        ro = nsw.Rollout(m, mean, std, w, clim=clim)
+        with torch.inference_mode():
+            torch.cuda.synchronize()
+            t0 = torch.cuda.Event(enable_timing=True); t1 = torch.cuda.Event(enable_timing=True)
+            t0.record(stream)
+            r, a, _ = ro.run(x, targets)
+            t1.record(stream)
+            torch.cuda.synchronize()
+        res[name] = (r.cpu().numpy(), a.cpu().numpy(), t0.elapsed_time(t1) / S)
+    rb, ab, msb = res["bf16"]
+    rf, af, msf = res["fp32"]
+    rollout = {
+        "workload": "config 5: config-3 model, 8 autoregressive steps from one seeded initial condition, "
+                    "per-step latitude-weighted RMSE and ACC over 70 channels (unnormalised fields)",
+        "steps": S, "ms_per_step_bf16": round(msb, 3), "ms_per_step_fp32": round(msf, 3),
+        "rmse_mean_bf16": [round(float(v), 6) for v in rb.mean(1)],
+        "rmse_rel_drift_max": [round(float(v), 6) for v in (np.abs(rb - rf) / rf).max(1)],
+        "acc_mean_bf16": [round(float(v), 6) for v in ab.mean(1)],
+        "acc_abs_drift_max": [round(float(v), 6) for v in np.abs(ab - af).max(1)],
+    }
+    return forecast, rollout
 
 
 def cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, target_s):
