@@ -77,6 +77,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-model", action="store_true", help="skip the config-3 forecast and config-5 rollout")
     ap.add_argument("--model-steps", type=int, default=10, help="timed forecast steps (config 3)")
+    ap.add_argument("--no-rollout", action="store_true", help="skip the config-5 rollout")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (5 launches): the reference kernel whose "
@@ -219,7 +220,9 @@ def main():
     if not args.no_model:
         del y, y2, qkv, o, h1, hn, u, xw
         torch.cuda.empty_cache()
-        out["forecast"], out["rollout"] = model_sections(dev, args.model_steps, args.warmup)
+        out["forecast"], rollout = model_sections(dev, args.model_steps, args.warmup, not args.no_rollout)
+        if rollout is not None:
+            out["rollout"] = rollout
 
     # ----------------------------------------------------------- CPU baseline
     if not args.no_cpu_baseline:
@@ -245,7 +248,7 @@ def smooth_fields(shape, sigma, seed, dev):
     return x
 
 
-def model_sections(dev, steps, warmup):
+def model_sections(dev, steps, warmup, with_rollout=True):
     """Config 3 (one forecast step of the d16 model) and config 5 (8-step
     rollout, bf16 vs fp32)."""
     import numpy as np
@@ -298,6 +301,8 @@ def model_sections(dev, steps, warmup):
         "head_ms": round(ev[2].elapsed_time(ev[3]), 3),
     }
     del tok, yb
+    if not with_rollout:
+        return forecast, None
 
     # config 5: rollout, bf16 and fp32 copies of the same weights
     S = 8

@@ -20,6 +20,8 @@
 // Unpatchify: out[b, c, i*p + u, j*p + v] = y[(b, i, j), (u*p + v)*C_out + c].
 #include "nsw_common.h"
 
+#include <algorithm>
+
 namespace nsw {
 
 constexpr int MODEL_LDS = 64 * 1024;   // dynamic LDS per workgroup
@@ -28,7 +30,7 @@ template <typename T> struct VecOf;
 template <> struct VecOf<bf16> { using V = bf16x8; };
 template <> struct VecOf<float> { using V = f32x4; };
 
-template <typename TX, typename TO>
+template <typename TX, typename TO, int P>
 __global__ __launch_bounds__(256) void im2col_kernel(const TX* __restrict__ x, const TX* __restrict__ inv,
                                                      int Cx, int Cinv, int T, int H, int W, int p,
                                                      int frame0, int Kp, int64_t M, int R,
@@ -63,19 +65,35 @@ __global__ __launch_bounds__(256) void im2col_kernel(const TX* __restrict__ x, c
   }
   __syncthreads();
 
-  // gather: lanes (r, v), one (c, u) pair per lane group and iteration
-  const int lanes = rows * p;
-  const int groups = 256 / (R * p);
-  const int lane = tid % (R * p), grp = tid / (R * p);
-  if (lane < lanes && grp < groups) {
-    const int r = lane / p, v = lane - r * p;
-    TO* trow = tile + r * KS + v;
-    for (int cu = grp; cu < C * p; cu += groups) {
-      const int c = cu / p, u = cu - c * p;
-      float val;
-      if (c < Cx) val = to_f32(x[xbase[r] + c * HW + (int64_t)u * W + v]);
-      else val = to_f32(inv[(int64_t)(c - Cx) * HW + ibase[r] + u * W + v]);
-      trow[cu * p] = from_f32<TO>(val);
+  // gather: one lane per tile row, one patch-row segment (p consecutive
+  // pixels, contiguous in x) per lane and iteration; the lane groups split
+  // the (c, u) pairs
+  const int groups = 256 / R;
+  const int r = tid % R, grp = tid / R;
+  if (r < rows && grp < groups) {
+    TO* trow = tile + r * KS;
+    const int64_t xb = xbase[r];
+    const int ib = ibase[r];
+    const int p_ = P > 0 ? P : p;
+#pragma unroll 4
+    for (int cu = grp; cu < C * p_; cu += groups) {
+      const int c = cu / p_, u = cu - c * p_;
+      const TX* src = c < Cx ? x + xb + c * HW + (int64_t)u * W : inv + (int64_t)(c - Cx) * HW + ib + u * W;
+      TO* dst = trow + cu * p_;
+      if constexpr (P > 0) {
+        // P consecutive elements, aligned to P * sizeof(T) (host-checked)
+        constexpr int SA = P * sizeof(TX) < 16 ? P * sizeof(TX) : 16;
+        constexpr int DA = P * sizeof(TO) < 16 ? P * sizeof(TO) : 16;
+        const TX* s_ = (const TX*)__builtin_assume_aligned(src, SA);
+        TO* d_ = (TO*)__builtin_assume_aligned(dst, DA);
+        TX v[P];
+#pragma unroll
+        for (int e = 0; e < P; ++e) v[e] = s_[e];
+#pragma unroll
+        for (int e = 0; e < P; ++e) d_[e] = from_f32<TO>(to_f32(v[e]));
+      } else {
+        for (int e = 0; e < p_; ++e) dst[e] = from_f32<TO>(to_f32(src[e]));
+      }
     }
   }
   // zero padding columns
@@ -96,7 +114,7 @@ __global__ __launch_bounds__(256) void im2col_kernel(const TX* __restrict__ x, c
   }
 }
 
-template <typename TI, typename TO>
+template <typename TI, typename TO, int P>
 __global__ __launch_bounds__(256) void unpatchify_kernel(const TI* __restrict__ y, int Co, int H, int W, int p,
                                                          int64_t out_bstride, int64_t M, int R,
                                                          TO* __restrict__ out) {
@@ -130,24 +148,39 @@ __global__ __launch_bounds__(256) void unpatchify_kernel(const TI* __restrict__ 
   }
   __syncthreads();
 
-  // scatter: lanes (r, v) write p consecutive pixels of adjacent patches
-  const int lanes = rows * p;
-  const int groups = 256 / (R * p);
-  const int lane = tid % (R * p), grp = tid / (R * p);
-  if (lane < lanes && grp < groups) {
-    const int r = lane / p, v = lane - r * p;
-    const TI* trow = tile + r * NS + v * Co;
-    for (int cu = grp; cu < Co * p; cu += groups) {
-      const int c = cu / p, u = cu - c * p;
-      out[obase[r] + c * HW + (int64_t)u * W + v] = from_f32<TO>(to_f32(trow[u * p * Co + c]));
+  // scatter: one lane per tile row; per iteration a lane writes the p
+  // consecutive pixels of its patch in one output row (one vector store)
+  const int groups = 256 / R;
+  const int r = tid % R, grp = tid / R;
+  if (r < rows && grp < groups) {
+    const int p_ = P > 0 ? P : p;
+    const TI* trow = tile + r * NS;
+    const int64_t ob = obase[r];
+#pragma unroll 4
+    for (int cu = grp; cu < Co * p_; cu += groups) {
+      const int c = cu / p_, u = cu - c * p_;
+      TO* dst = out + ob + c * HW + (int64_t)u * W;
+      const TI* src = trow + u * p_ * Co + c;
+      if constexpr (P > 0) {
+        constexpr int DA = P * sizeof(TO) < 16 ? P * sizeof(TO) : 16;
+        TO* d_ = (TO*)__builtin_assume_aligned(dst, DA);
+        TO v[P];
+#pragma unroll
+        for (int e = 0; e < P; ++e) v[e] = from_f32<TO>(to_f32(src[e * Co]));
+#pragma unroll
+        for (int e = 0; e < P; ++e) d_[e] = v[e];
+      } else {
+        for (int e = 0; e < p_; ++e) dst[e] = from_f32<TO>(to_f32(src[e * Co]));
+      }
     }
   }
 }
 
-// Rows per workgroup: at most 256 / p (one lane per pixel of a patch row
-// segment) and at most MODEL_LDS of tile.
+// Rows per workgroup: at most 64 (four lane groups split the (c, u) pairs)
+// and at most MODEL_LDS of tile.
 static int rows_per_wg(int p, int row_bytes) {
-  int r = 256 / p;
+  (void)p;
+  int r = 64;
   const int lim = MODEL_LDS / row_bytes;
   if (lim < r) r = lim;
   return r < 1 ? 1 : r;
@@ -183,14 +216,29 @@ extern "C" int nsw_patch_im2col(const void* x, const void* inv, int64_t B, int64
   hipStream_t st = (hipStream_t)stream;
   const size_t shm = (size_t)R * row_bytes;
   const dim3 g((unsigned)grid), blk(256);
-#define NSW_IM2COL(TX, TO)                                                                              \
-  hipLaunchKernelGGL((im2col_kernel<TX, TO>), g, blk, shm, st, (const TX*)x, (const TX*)inv, (int)C_x, \
+  // p-specialised instances move one aligned vector per patch-row segment
+  const size_t xes = dtype_size(x_dtype);
+  const bool vec = (p == 1 || p == 2 || p == 4 || p == 8 || p == 16) &&
+                   ((uintptr_t)x % std::min<size_t>(16, p * xes)) == 0 &&
+                   (inv == nullptr || ((uintptr_t)inv % std::min<size_t>(16, p * xes)) == 0);
+#define NSW_IM2COL_P(TX, TO, P)                                                                              \
+  hipLaunchKernelGGL((im2col_kernel<TX, TO, P>), g, blk, shm, st, (const TX*)x, (const TX*)inv, (int)C_x,   \
                      (int)C_inv, (int)T, (int)H, (int)W, (int)p, (int)frame0, (int)Kp, M, R, (TO*)out)
+#define NSW_IM2COL(TX, TO)                                                                                   \
+  do {                                                                                                       \
+    if (!vec) NSW_IM2COL_P(TX, TO, 0);                                                                       \
+    else if (p == 1) NSW_IM2COL_P(TX, TO, 1);                                                                \
+    else if (p == 2) NSW_IM2COL_P(TX, TO, 2);                                                                \
+    else if (p == 4) NSW_IM2COL_P(TX, TO, 4);                                                                \
+    else if (p == 8) NSW_IM2COL_P(TX, TO, 8);                                                                \
+    else NSW_IM2COL_P(TX, TO, 16);                                                                           \
+  } while (0)
   if (x_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_BF16) NSW_IM2COL(float, bf16);
   else if (x_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_F32) NSW_IM2COL(float, float);
   else if (x_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_BF16) NSW_IM2COL(bf16, bf16);
   else if (x_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_F32) NSW_IM2COL(bf16, float);
   else return set_error(NSW_ERR_INVALID, "%s: unknown dtype pair %d -> %d", what, x_dtype, out_dtype);
+#undef NSW_IM2COL_P
 #undef NSW_IM2COL
   return check_launch(what);
 }
@@ -217,14 +265,28 @@ extern "C" int nsw_unpatchify(const void* y, void* out, int64_t B, int64_t C_out
   hipStream_t st = (hipStream_t)stream;
   const size_t shm = (size_t)R * row_bytes;
   const dim3 g((unsigned)grid), blk(256);
-#define NSW_UNPATCH(TI, TO)                                                                           \
-  hipLaunchKernelGGL((unpatchify_kernel<TI, TO>), g, blk, shm, st, (const TI*)y, (int)C_out, (int)H, \
+  const size_t oes = dtype_size(out_dtype);
+  const bool vec = (p == 1 || p == 2 || p == 4 || p == 8 || p == 16) &&
+                   ((uintptr_t)out % std::min<size_t>(16, p * oes)) == 0 &&
+                   ((out_bstride * (int64_t)oes) % (int64_t)std::min<size_t>(16, p * oes)) == 0;
+#define NSW_UNPATCH_P(TI, TO, P)                                                                           \
+  hipLaunchKernelGGL((unpatchify_kernel<TI, TO, P>), g, blk, shm, st, (const TI*)y, (int)C_out, (int)H,    \
                      (int)W, (int)p, out_bstride, M, R, (TO*)out)
+#define NSW_UNPATCH(TI, TO)                                                                                \
+  do {                                                                                                     \
+    if (!vec) NSW_UNPATCH_P(TI, TO, 0);                                                                    \
+    else if (p == 1) NSW_UNPATCH_P(TI, TO, 1);                                                             \
+    else if (p == 2) NSW_UNPATCH_P(TI, TO, 2);                                                             \
+    else if (p == 4) NSW_UNPATCH_P(TI, TO, 4);                                                             \
+    else if (p == 8) NSW_UNPATCH_P(TI, TO, 8);                                                             \
+    else NSW_UNPATCH_P(TI, TO, 16);                                                                        \
+  } while (0)
   if (in_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_BF16) NSW_UNPATCH(bf16, bf16);
   else if (in_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_F32) NSW_UNPATCH(bf16, float);
   else if (in_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_F32) NSW_UNPATCH(float, float);
   else if (in_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_BF16) NSW_UNPATCH(float, bf16);
   else return set_error(NSW_ERR_INVALID, "%s: unknown dtype pair %d -> %d", what, in_dtype, out_dtype);
+#undef NSW_UNPATCH_P
 #undef NSW_UNPATCH
   return check_launch(what);
 }
