@@ -87,3 +87,31 @@ def test_mlp_rejects_unfusable_activation():
     m = MLP(16, 32, act_layer=torch.nn.ReLU)
     with pytest.raises(NotImplementedError):
         m._check_fusable()
+
+
+def test_full_model_te_checkpoint_loads_into_swin_transformer(tmp_path):
+    """A reference checkpoint of the whole model in production layout (TE block
+    names, DDP + TimeStepper prefixes, TE _extra_state entries) saved as
+    {"model_state": ...} loads through the safe loader into nsw.SwinTransformer
+    with every tensor in place (models/helpers.py:53-70, tests/test_te.py:34-71)."""
+    import torch
+    import nsw
+    from nsw import checkpoint
+    from oracle import synth
+    C, E, depth, heads, p, H, W = 6, 64, 2, 4, 2, 36, 72
+    prm = synth.model_params(C, C, E, depth, heads, p, seed=11, random_bias=True, random_norm=True)
+    te = checkpoint.vanilla_to_te(prm)
+    state = {"module.model." + k: v for k, v in te.items()}
+    state["module.model.blocks.0.rms_norm_mlp._extra_state"] = torch.zeros(3)
+    state["module.model.blocks.1.attn.q._extra_state"] = torch.zeros(2)
+    path = tmp_path / "ckpt_best.tar"
+    torch.save({"model_state": state, "epoch": 3}, path)
+    loaded = checkpoint.load_checkpoint_model_state(str(path))
+    meta = {"coords": torch.rand(H, W, 3), "sp_shapes": [[H], [W]], "n_channels": C}
+    model = nsw.SwinTransformer(temporal_context_window_size=1, window_size=(9, 18), patch_size=p, in_chans=C,
+                                out_chans=C, embed_dim=E, depth=depth, num_heads=heads, domain_metadata=meta)
+    model.load_state_dict(loaded, strict=True)
+    sd = model.state_dict()
+    assert set(sd) == set(prm)
+    for k, v in prm.items():
+        assert torch.equal(sd[k], v), k
