@@ -78,6 +78,9 @@ def main():
     ap.add_argument("--no-model", action="store_true", help="skip the config-3 forecast and config-5 rollout")
     ap.add_argument("--model-steps", type=int, default=10, help="timed forecast steps (config 3)")
     ap.add_argument("--no-rollout", action="store_true", help="skip the config-5 rollout")
+    ap.add_argument("--fused-norms", action="store_true",
+                    help="fold the block's two RMSNorms into the GEMMs that consume them (5 launches "
+                         "instead of 7; slower on MI355X, kept as an ablation)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (5 launches): the reference kernel whose "
@@ -110,6 +113,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.manual_seed(1001)
     blk = nsw.Block(C, heads, (H, W), ws, T, shift_size=shift).to(device=dev, dtype=dtype).eval()
+    blk.fuse_norms = args.fused_norms
     g = torch.Generator().manual_seed(1002)
     x = torch.randn(B, T, H, W, C, generator=g).to(device=dev, dtype=dtype)
     M = B * T * H * W
@@ -138,25 +142,43 @@ def main():
         # them on the launch stream
         pk = blk.packed()
         eps = blk._eps(dtype)
-        names = ["gather_norm1", "qkv", "attention", "proj_scatter", "norm2", "fc1", "fc2"]
+        if blk.fuse_norms:
+            names = ["qkv_norm_gather", "attention", "proj_scatter", "fc1_rownorm", "fc2"]
+        else:
+            names = ["gather_norm1", "qkv", "attention", "proj_scatter", "norm2", "fc1", "fc2"]
         times = {n: [] for n in names}
         for it in range(args.warmup + args.steps):
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
-            ev[0].record(stream)
-            xw = ops.rmsnorm_roll_partition(x, pk["norm1_w"], ws, shift, eps)
-            ev[1].record(stream)
-            qkv = ops.qkv_projection(xw, pk["wqkv"], pk["bqkv"], pk["qn_w"], pk["kn_w"], heads, eps)
-            ev[2].record(stream)
+            k = 0
+            ev[k].record(stream)
+            if blk.fuse_norms:
+                qkv = ops.qkv_projection_norm_gather(x, pk["wqkv_n1"], pk["bqkv"], pk["qn_w"], pk["kn_w"],
+                                                     heads, ws, shift, eps)
+            else:
+                xw = ops.rmsnorm_roll_partition(x, pk["norm1_w"], ws, shift, eps)
+                k += 1
+                ev[k].record(stream)
+                qkv = ops.qkv_projection(xw, pk["wqkv"], pk["bqkv"], pk["qn_w"], pk["kn_w"], heads, eps)
+            k += 1
+            ev[k].record(stream)
             o = ops.window_attention(qkv, heads, (C // heads) ** -0.5, geometry=(H, W, ws, shift, T))
-            ev[3].record(stream)
+            k += 1
+            ev[k].record(stream)
             h1 = ops.proj_reverse_residual(o, pk["wproj"], pk["bproj"], x, ws, shift)
-            ev[4].record(stream)
-            hn = ops.rms_norm(h1, pk["norm2_w"], eps)
-            ev[5].record(stream)
-            u = ops.linear(hn, pk["w1"], pk["b1"], epilogue=_lib.NSW_EPI_BIAS_GELU)
-            ev[6].record(stream)
+            k += 1
+            ev[k].record(stream)
+            if blk.fuse_norms:
+                u = ops.linear_rownorm(h1, pk["w1_n2"], pk["b1"], epilogue=_lib.NSW_EPI_BIAS_GELU, eps=eps)
+            else:
+                hn = ops.rms_norm(h1, pk["norm2_w"], eps)
+                k += 1
+                ev[k].record(stream)
+                u = ops.linear(hn, pk["w1"], pk["b1"], epilogue=_lib.NSW_EPI_BIAS_GELU)
+            k += 1
+            ev[k].record(stream)
             y2 = ops.linear(u, pk["w2"], pk["b2"], residual=h1)
-            ev[7].record(stream)
+            k += 1
+            ev[k].record(stream)
             torch.cuda.synchronize()
             if it >= args.warmup:
                 for i, n in enumerate(names):
@@ -170,7 +192,7 @@ def main():
     work = {  # (algorithmic units per launch, bound)
         "gather_norm1": (2 * A, "hbm"), "qkv": (fl["qkv"], "mfma"), "attention": (4 * A, "hbm"),
         "proj_scatter": (fl["proj"], "mfma"), "norm2": (2 * A, "hbm"), "fc1": (fl["fc1"], "mfma"),
-        "fc2": (fl["fc2"], "mfma"),
+        "fc2": (fl["fc2"], "mfma"), "qkv_norm_gather": (fl["qkv"], "mfma"), "fc1_rownorm": (fl["fc1"], "mfma"),
     }
     kern = {}
     for n in names:
@@ -211,14 +233,15 @@ def main():
         "data": "synthetic (N(0,1) activations, reference trunc-normal(0.02) weights)",
         "config": {"workload": desc, "tokens": M, "block_tflop": round(total_flops / 1e12, 4),
                    "block_tflops_achieved": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
-                   "wall_s_timed": round(wall, 4), "ops_path_equals_fused": bool(same)},
+                   "wall_s_timed": round(wall, 4), "ops_path_equals_fused": bool(same),
+                   "block_launches": len(names)},
         "roofline": roofline,
         "kernels": kern,
     }
 
     # ------------------------------------------------- config 3 / config 5
     if not args.no_model:
-        del y, y2, qkv, o, h1, hn, u, xw
+        del y, y2, qkv, o, h1, u
         torch.cuda.empty_cache()
         out["forecast"], rollout = model_sections(dev, args.model_steps, args.warmup, not args.no_rollout)
         if rollout is not None:

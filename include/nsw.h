@@ -142,6 +142,15 @@ typedef struct nsw_block_params {
   const void* b1;        /* [Hm]         mlp.bias1.bias                         */
   const void* w2;        /* [C, Hm]      mlp.fc2.weight                         */
   const void* b2;        /* [C]          mlp.bias2.bias                         */
+  /* Optional norm-folded weights (both or neither): wqkv_n1[n,k] =
+   * wqkv[n,k] * norm1_w[k], w1_n2[n,k] = w1[n,k] * norm2_w[k].  When given,
+   * the two RMSNorms run inside the GEMMs that consume them (5 launches:
+   * nsw_qkv_projection_norm_gather, attention, proj scatter,
+   * nsw_linear_rownorm, fc2) instead of as separate passes (7 launches).
+   * The 7-launch form is the faster one on MI355X (the row sums add VALU work
+   * to the GEMM main loop); the folded form is kept as an option. */
+  const void* wqkv_n1;   /* [3C, C] or NULL                                     */
+  const void* w1_n2;     /* [Hm, C] or NULL                                     */
 } nsw_block_params;
 
 typedef struct nsw_block_shape {
@@ -186,6 +195,29 @@ int nsw_weighted_metrics_unnorm(const void* pred, int pred_dtype, const float* t
                                 int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
                                 int64_t Cch, double* rmse, double* acc, void* workspace,
                                 size_t workspace_bytes, void* stream);
+
+/* Block.forward's first half with norm1 fused (models/swin_helpers.py:446 +
+ * :402-412 + WindowMultiHeadAttention.forward :212-241): qkv[m] (window order,
+ * [B*nW*T*wa, 3C]) = per-head-q/k-RMSNorm(rs[t] * (x[t] . wqkv_n^T) + bqkv) with
+ * t = token of window row m (roll by -shift + window_partition),
+ * rs[t] = 1/sqrt(mean_c x[t,c]^2 + eps) and wqkv_n = wqkv * norm1_w per input
+ * column: the same value as nsw_rmsnorm_roll_partition followed by
+ * nsw_qkv_projection, in one GEMM whose copies gather the token rows.
+ * x [B,T,H,W,C].  Requires C % 64 == 0, hd in {16,32,64}. */
+int nsw_qkv_projection_norm_gather(const void* x, const void* wqkv_n, const void* bqkv,
+                                   const void* qn_w, const void* kn_w, float eps, void* qkv,
+                                   int64_t B, int64_t T, int64_t H, int64_t W, int64_t C,
+                                   int64_t num_heads, int64_t ws0, int64_t ws1, int64_t s0,
+                                   int64_t s1, int dtype, void* stream);
+
+/* y = epi(RMSNorm(x; norm_w, eps) . W^T) (Block.forward's norm2 + MLP fc1,
+ * models/swin_helpers.py:457, models/mlp.py:80-85) as one GEMM: w_n[n,k] =
+ * W[n,k] * norm_w[k]; the row norms of x are accumulated from the GEMM's own
+ * x fragments and applied before the bias.  Epilogues and requirements as
+ * nsw_linear. */
+int nsw_linear_rownorm(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
+                       int64_t M, int64_t N, int64_t K, int epilogue, float eps, int dtype,
+                       void* stream);
 
 /* Patch matrix of the stride-p patch convolution (PatchEmbedLayer,
  * models/layer_helpers.py:120-172, as called by SwinTransformer.prepare_tokens,

@@ -8,6 +8,15 @@
 //   K6  u   = gelu(hn . W1^T + b1)                                 (MFMA GEMM)
 //   K7  y   = u . W2^T + b2 + h1                                   (MFMA GEMM)
 //
+// With the norm-folded weights (p->wqkv_n1, p->w1_n2) K1 and K5 disappear
+// into the GEMMs that consume them:
+//
+//   K2' qkv = per-head-norm(rs1 . (gather(x) . (Wqkv*norm1)^T) + b)
+//   K6' u   = gelu(rs2 . (h1 . (W1*norm2)^T) + b1)
+//
+// with rs the rows' 1/sqrt(mean square + eps), accumulated from the GEMMs'
+// own x / h1 fragments (5 launches).
+//
 // Workspace (dtype elements): A [M*C] holds xw, then o, then hn; Q [M*max(3C,
 // Hm)] holds qkv, then u; H1 [M*C] holds h1.  M = B*T*H*W tokens.
 #include "nsw_common.h"
@@ -18,6 +27,12 @@ int gemm_qkv(const void* x, const void* wqkv, const void* bqkv, const void* qn_w
 int gemm_proj_scatter(const void* o, const void* wproj, const void* bproj, const void* skip, void* y,
                       int64_t B, int64_t T, int64_t H, int64_t W, int64_t C, int64_t ws0, int64_t ws1,
                       int64_t s0, int64_t s1, int dtype, void* stream);
+int gemm_qkv_norm_gather(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w,
+                         const void* kn_w, float eps, void* qkv, int64_t B, int64_t T, int64_t H, int64_t W,
+                         int64_t C, int64_t num_heads, int64_t ws0, int64_t ws1, int64_t s0, int64_t s1,
+                         int dtype, void* stream);
+int gemm_linear_rownorm(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
+                        int64_t M, int64_t N, int64_t K, int epilogue, float eps, int dtype, void* stream);
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -66,6 +81,28 @@ extern "C" int nsw_swin_block_forward(const void* x, void* y, const nsw_block_pa
   const int64_t L = s->T * s->ws0 * s->ws1;
   const int64_t hd = C / s->num_heads;
   int rc;
+  NSW_CHECK_ARG((p->wqkv_n1 == nullptr) == (p->w1_n2 == nullptr), "%s: give both norm-folded weights or neither",
+                what);
+  if (p->wqkv_n1) {
+    // K2'
+    rc = gemm_qkv_norm_gather(x, p->wqkv_n1, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, s->B, s->T, s->H, s->W, C,
+                              s->num_heads, s->ws0, s->ws1, s->s0, s->s1, s->dtype, stream);
+    if (rc) return rc;
+    // K3
+    rc = nsw_window_attention(Q, A, nullptr, 0, M / L, L, C, s->num_heads, 1.0f / sqrtf((float)hd), s->H,
+                              s->W, s->ws0, s->ws1, s->s0, s->s1, s->T, s->dtype, stream);
+    if (rc) return rc;
+    // K4
+    rc = gemm_proj_scatter(A, p->wproj, p->bproj, x, H1, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1, s->s0,
+                           s->s1, s->dtype, stream);
+    if (rc) return rc;
+    // K6' (u overwrites qkv in Q)
+    rc = gemm_linear_rownorm(H1, p->w1_n2, p->b1, nullptr, Q, M, s->hidden, C, NSW_EPI_BIAS_GELU, s->eps,
+                             s->dtype, stream);
+    if (rc) return rc;
+    // K7
+    return nsw_linear(Q, p->w2, p->b2, H1, y, M, C, s->hidden, NSW_EPI_BIAS_RESIDUAL, s->dtype, stream);
+  }
   // K1
   rc = nsw_rmsnorm_roll_partition(x, p->norm1_w, s->eps, A, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1,
                                   s->s0, s->s1, s->dtype, stream);

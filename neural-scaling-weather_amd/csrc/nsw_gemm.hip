@@ -61,6 +61,19 @@ enum Epi {
   EPI_QKV_HN64 = 64
 };
 
+// Operand-side fusions (template parameter PRE):
+//   PRE_NONE     y = epi(x . w^T)
+//   PRE_ROWNORM  y = epi(rs . (x . w^T)) with rs[m] = 1/sqrt(mean_k x[m,k]^2 + eps):
+//                the RMSNorm of the rows of x with its weight folded into w
+//                (w[n,k] = W[n,k] * norm_w[k], prepared by the caller), so
+//                that x . w^T * rs = RMSNorm(x) . W^T.  The sums of squares
+//                are accumulated from the x fragments the MFMAs consume
+//                (v_dot2c_f32_bf16 / FMA), rs is applied before the bias.
+//   PRE_ROWNORM_GATHER  as PRE_ROWNORM, and the copy of x row m reads token
+//                row token_of_row(m) of the image (roll by -shift + window
+//                partition folded into the copy addresses).
+enum Pre { PRE_NONE = 0, PRE_ROWNORM = 1, PRE_ROWNORM_GATHER = 2 };
+
 constexpr int qkv_head_dim(int epi) {
   return (epi == EPI_QKV_HN16 || epi == EPI_QKV_HN32 || epi == EPI_QKV_HN64) ? epi : 0;
 }
@@ -152,6 +165,26 @@ __device__ __forceinline__ void mfma_chunk(f32x4& acc, const u32x4& a, const u32
   }
 }
 
+// Sum of squares of the 8 bf16 (4 f32) values of one 16-byte fragment, added to s.
+// bf16: v_dot2c_f32_bf16 (s += lo*lo + hi*hi) per dword, issued through inline
+// asm: with the builtin (ROCm 7.2 clang) the four dword extracts of the
+// fragment were folded into the first one (every dot2 read dword 0).
+template <typename T>
+__device__ __forceinline__ float frag_sumsq(const u32x4& f, float s) {
+  if constexpr (sizeof(T) == 2) {
+    const uint32_t d0 = f[0], d1 = f[1], d2 = f[2], d3 = f[3];
+    asm("v_dot2c_f32_bf16 %0, %1, %1" : "+v"(s) : "v"(d0));
+    asm("v_dot2c_f32_bf16 %0, %1, %1" : "+v"(s) : "v"(d1));
+    asm("v_dot2c_f32_bf16 %0, %1, %1" : "+v"(s) : "v"(d2));
+    asm("v_dot2c_f32_bf16 %0, %1, %1" : "+v"(s) : "v"(d3));
+  } else {
+    const f32x4 v = __builtin_bit_cast(f32x4, f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = fmaf(v[i], v[i], s);
+  }
+  return s;
+}
+
 // Bijective remap of the hardware workgroup id so that XCD x (which receives
 // ids x, x+8, x+16, ...) processes the contiguous logical range
 // [x*q + min(x, rem), ...); GROUP_M row blocks per tile group.
@@ -236,7 +269,7 @@ __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk)
   return *reinterpret_cast<const u32x4*>(stage + row * ROWB + slot * 16);
 }
 
-template <typename T, int EPI, int TN>
+template <typename T, int EPI, int TN, int PRE>
 __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* __restrict__ X,
                                                                       const T* __restrict__ Wt,
                                                                       T* __restrict__ Y, int M, int N,
@@ -286,6 +319,9 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
       int g = xside ? m0 + srow : n0 + srow - BM;
       const int lim = xside ? M : N;
       g = g < lim ? g : lim - 1;   // rows past the edge re-read the last row (never stored)
+      if constexpr (PRE == PRE_ROWNORM_GATHER) {
+        if (xside) g = (int)ea.geom.token_of_row(g);
+      }
       cp.voff[j] = (uint32_t)g * rowbytes + chunk * 16;
     }
   }
@@ -302,6 +338,9 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   const int nk = K / (STEPB / (int)sizeof(T));   // MFMA steps
   const int nst = nk / SUB;                       // LDS stages
   u32x4 fa[2][NB], fb[2][MB];
+  float ssr[MB];                                  // PRE: this lane's part of the row sums of squares
+#pragma unroll
+  for (int i = 0; i < MB; ++i) ssr[i] = 0.f;
 
 #define NSW_STAGE(i) (smem + ((i) % NSTAGE) * STAGE_BYTES)
 #define NSW_WAIT_AHEAD(ahead)                                                                  \
@@ -347,6 +386,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
         if (mb < NB) fa[(U + 1) & 1][mb] = lds_frag<ROWB>(nx, arow + mb * 16, nch_ + fg);      \
         _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                      \
           mfma_chunk<T>(acc[nb][mb], fa[U & 1][nb], fb[U & 1][mb]);                            \
+        if constexpr (PRE != PRE_NONE) ssr[mb] = frag_sumsq<T>(fb[U & 1][mb], ssr[mb]);        \
         if (mb < NB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                        \
         else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                \
         __builtin_amdgcn_sched_group_barrier(0x008, NB * (sizeof(T) == 2 ? 1 : 4), 0);         \
@@ -410,6 +450,14 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
     }
   }
 
+  // PRE: the four lane groups hold the four k chunks of each x row
+  float rsr[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    rsr[mb] = 1.f;
+    if constexpr (PRE != PRE_NONE) rsr[mb] = 1.0f / sqrtf(rows4_sum(ssr[mb]) / (float)K + ea.eps);
+  }
+
   // 1. epilogue math in the fragment layout, in place
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -417,7 +465,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[nb][r] = acc[nb][mb][r] + bv[nb][r];
+      for (int r = 0; r < 4; ++r) v[nb][r] = (PRE != PRE_NONE ? acc[nb][mb][r] * rsr[mb] : acc[nb][mb][r]) + bv[nb][r];
 
     if constexpr (HDQ > 0) {
       // sum of squares of each head: local over its blocks, then across the
@@ -530,15 +578,15 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   }
 }
 
-template <typename T, int EPI, int TN>
+template <typename T, int EPI, int TN, int PRE>
 static void launch_tiles(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
                          const EpiArgs& ea, hipStream_t st) {
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + TN - 1) / TN);
-  hipLaunchKernelGGL((gemm_kernel<T, EPI, TN>), dim3((unsigned)tiles), dim3(256), 0, st, (const T*)x,
+  hipLaunchKernelGGL((gemm_kernel<T, EPI, TN, PRE>), dim3((unsigned)tiles), dim3(256), 0, st, (const T*)x,
                      (const T*)w, (T*)y, (int)M, (int)N, (int)K, ea);
 }
 
-template <typename T, int EPI>
+template <typename T, int EPI, int PRE = PRE_NONE>
 static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
                        const EpiArgs& ea, hipStream_t st, const char* what) {
   constexpr int KT = 128 / sizeof(T);
@@ -556,17 +604,17 @@ static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t
   // two workgroups per CU overlap one tile's epilogue with the other's MFMAs.
   // Otherwise the 256x256 main loop.
   constexpr bool heavy = EPI == EPI_BIAS_GELU || EPI == EPI_SCATTER_RESIDUAL || qkv_head_dim(EPI) > 0;
-  if (heavy && K <= 2048) launch_tiles<T, EPI, 128>(x, w, y, M, N, K, ea, st);
-  else launch_tiles<T, EPI, 256>(x, w, y, M, N, K, ea, st);
+  if (heavy && K <= 2048) launch_tiles<T, EPI, 128, PRE>(x, w, y, M, N, K, ea, st);
+  else launch_tiles<T, EPI, 256, PRE>(x, w, y, M, N, K, ea, st);
   return check_launch(what);
 }
 
-template <int EPI>
+template <int EPI, int PRE = PRE_NONE>
 static int dispatch_gemm(int dtype, const void* x, const void* w, void* y, int64_t M, int64_t N,
                          int64_t K, const EpiArgs& ea, void* stream, const char* what) {
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == NSW_DTYPE_BF16) return launch_gemm<bf16, EPI>(x, w, y, M, N, K, ea, st, what);
-  if (dtype == NSW_DTYPE_F32) return launch_gemm<float, EPI>(x, w, y, M, N, K, ea, st, what);
+  if (dtype == NSW_DTYPE_BF16) return launch_gemm<bf16, EPI, PRE>(x, w, y, M, N, K, ea, st, what);
+  if (dtype == NSW_DTYPE_F32) return launch_gemm<float, EPI, PRE>(x, w, y, M, N, K, ea, st, what);
   return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, dtype);
 }
 
@@ -603,9 +651,72 @@ int gemm_proj_scatter(const void* o, const void* wproj, const void* bproj, const
   return dispatch_gemm<EPI_SCATTER_RESIDUAL>(dtype, o, wproj, y, B * T * H * W, C, C, ea, stream, what);
 }
 
+// QKV projection of RMSNorm(x) gathered into window order: qkv[m] =
+// headnorm(rs[t] * (x[t] . wqkv_n^T) + bqkv), t = token_of_row(m),
+// wqkv_n = wqkv * norm1_w (per input column, prepared by the caller).
+int gemm_qkv_norm_gather(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w,
+                         const void* kn_w, float eps, void* qkv, int64_t B, int64_t T, int64_t H, int64_t W,
+                         int64_t C, int64_t num_heads, int64_t ws0, int64_t ws1, int64_t s0, int64_t s1,
+                         int dtype, void* stream) {
+  const char* what = "nsw_qkv_projection_norm_gather";
+  int rc = check_geom(B, T, H, W, ws0, ws1, what);
+  if (rc) return rc;
+  NSW_CHECK_ARG(num_heads > 0 && C % num_heads == 0, "%s: C=%lld not divisible by num_heads=%lld", what,
+                (long long)C, (long long)num_heads);
+  const int64_t hd = C / num_heads;
+  NSW_CHECK_ARG(C % 64 == 0, "%s: C=%lld must be a multiple of 64", what, (long long)C);
+  NSW_CHECK_ARG(hd == 16 || hd == 32 || hd == 64, "%s: head_dim=%lld unsupported (16, 32, 64)", what,
+                (long long)hd);
+  NSW_CHECK_ARG(bqkv && qn_w && kn_w, "%s: bias and norm weights are required", what);
+  NSW_CHECK_ARG(x != (const void*)qkv, "%s: x and qkv must not alias", what);
+  EpiArgs ea{};
+  ea.bias = bqkv; ea.qn_w = qn_w; ea.kn_w = kn_w; ea.eps = eps; ea.C = (int)C;
+  ea.geom = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
+  const int64_t M = B * T * H * W;
+  if (hd == 64)
+    return dispatch_gemm<EPI_QKV_HN64, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+  if (hd == 32)
+    return dispatch_gemm<EPI_QKV_HN32, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+  return dispatch_gemm<EPI_QKV_HN16, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+}
+
+// y = epi(RMSNorm(x) . W^T) with w_n = W * norm_w: the row norm of x fused.
+int gemm_linear_rownorm(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
+                        int64_t M, int64_t N, int64_t K, int epilogue, float eps, int dtype, void* stream) {
+  const char* what = "nsw_linear_rownorm";
+  EpiArgs ea{};
+  ea.bias = bias; ea.residual = residual; ea.eps = eps;
+  if (epilogue != NSW_EPI_NONE) NSW_CHECK_ARG(bias != nullptr, "%s: epilogue %d needs a bias", what, epilogue);
+  switch (epilogue) {
+    case NSW_EPI_NONE: return dispatch_gemm<EPI_NONE, PRE_ROWNORM>(dtype, x, w_n, y, M, N, K, ea, stream, what);
+    case NSW_EPI_BIAS: return dispatch_gemm<EPI_BIAS, PRE_ROWNORM>(dtype, x, w_n, y, M, N, K, ea, stream, what);
+    case NSW_EPI_BIAS_GELU:
+      return dispatch_gemm<EPI_BIAS_GELU, PRE_ROWNORM>(dtype, x, w_n, y, M, N, K, ea, stream, what);
+    case NSW_EPI_BIAS_RESIDUAL:
+      NSW_CHECK_ARG(residual != nullptr, "%s: residual epilogue needs a residual", what);
+      return dispatch_gemm<EPI_BIAS_RESIDUAL, PRE_ROWNORM>(dtype, x, w_n, y, M, N, K, ea, stream, what);
+    default: return set_error(NSW_ERR_INVALID, "%s: unknown epilogue %d", what, epilogue);
+  }
+}
+
 }  // namespace nsw
 
 using namespace nsw;
+
+extern "C" int nsw_qkv_projection_norm_gather(const void* x, const void* wqkv_n, const void* bqkv,
+                                              const void* qn_w, const void* kn_w, float eps, void* qkv,
+                                              int64_t B, int64_t T, int64_t H, int64_t W, int64_t C,
+                                              int64_t num_heads, int64_t ws0, int64_t ws1, int64_t s0,
+                                              int64_t s1, int dtype, void* stream) {
+  return gemm_qkv_norm_gather(x, wqkv_n, bqkv, qn_w, kn_w, eps, qkv, B, T, H, W, C, num_heads, ws0, ws1, s0, s1,
+                              dtype, stream);
+}
+
+extern "C" int nsw_linear_rownorm(const void* x, const void* w_n, const void* bias, const void* residual,
+                                  void* y, int64_t M, int64_t N, int64_t K, int epilogue, float eps, int dtype,
+                                  void* stream) {
+  return gemm_linear_rownorm(x, w_n, bias, residual, y, M, N, K, epilogue, eps, dtype, stream);
+}
 
 extern "C" int nsw_linear(const void* x, const void* w, const void* bias, const void* residual, void* y,
                           int64_t M, int64_t N, int64_t K, int epilogue, int dtype, void* stream) {

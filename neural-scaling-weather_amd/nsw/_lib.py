@@ -33,7 +33,7 @@ _int = ctypes.c_int
 class BlockParams(ctypes.Structure):
     _fields_ = [(n, _vp) for n in (
         "norm1_w", "wqkv", "bqkv", "qn_w", "kn_w", "wproj", "bproj",
-        "norm2_w", "w1", "b1", "w2", "b2")]
+        "norm2_w", "w1", "b1", "w2", "b2", "wqkv_n1", "w1_n2")]
 
 
 class BlockShape(ctypes.Structure):
@@ -71,6 +71,9 @@ SIGNATURES = {
                                     ctypes.c_size_t, _vp]),
     "nsw_weighted_metrics_unnorm": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
                                            _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "nsw_qkv_projection_norm_gather": (_int, [_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _i64, _i64, _i64, _i64,
+                                              _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+    "nsw_linear_rownorm": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _f32, _int, _vp]),
     "nsw_patch_im2col": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _int,
                                 _int, _vp]),
     "nsw_unpatchify": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),

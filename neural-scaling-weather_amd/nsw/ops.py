@@ -214,6 +214,47 @@ def qkv_projection(x: torch.Tensor, wqkv: torch.Tensor, bqkv: torch.Tensor, qn_w
 
 # --------------------------------------------------------------- attention ---
 
+def qkv_projection_norm_gather(x: torch.Tensor, wqkv_n: torch.Tensor, bqkv: torch.Tensor, qn_w: torch.Tensor,
+                               kn_w: torch.Tensor, num_heads: int, window_size, shift_size,
+                               eps: Optional[float] = None) -> torch.Tensor:
+    """x [B,T,H,W,C] (token order) -> qkv [B*nW, T*wa, 3C] (window order):
+    RMSNorm (weight folded into wqkv_n), roll + partition and the QKV
+    projection with per-head q/k RMSNorm in one GEMM."""
+    dev = _dev(x, wqkv_n, bqkv, qn_w, kn_w)
+    _same_dtype(x, wqkv_n, bqkv, qn_w, kn_w)
+    B, T, H, W, C = x.shape
+    eps = default_eps(x.dtype) if eps is None else float(eps)
+    ws0, ws1 = window_size
+    y = torch.empty(B * (H // ws0) * (W // ws1), T * ws0 * ws1, 3 * C, dtype=x.dtype, device=dev)
+    check(lib().nsw_qkv_projection_norm_gather(x.data_ptr(), wqkv_n.data_ptr(), bqkv.data_ptr(), qn_w.data_ptr(),
+                                               kn_w.data_ptr(), eps, y.data_ptr(), B, T, H, W, C, num_heads,
+                                               window_size[0], window_size[1], shift_size[0], shift_size[1],
+                                               dtype_code(x), _stream(dev)), "qkv_projection_norm_gather")
+    return y
+
+
+def linear_rownorm(x: torch.Tensor, w_n: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                   residual: Optional[torch.Tensor] = None, epilogue: Optional[int] = None,
+                   eps: Optional[float] = None) -> torch.Tensor:
+    """y = epi(RMSNorm(x) . W^T) with w_n = W * norm_w (the norm weight
+    folded in), the row norms of x computed inside the GEMM."""
+    dev = _dev(x, w_n, bias, residual)
+    _same_dtype(x, w_n, bias, residual)
+    K = x.shape[-1]
+    N, Kw = w_n.shape
+    if Kw != K:
+        raise ValueError(f"linear_rownorm: x has {K} features, weight expects {Kw}")
+    M = x.numel() // K
+    if epilogue is None:
+        epilogue = _lib.NSW_EPI_NONE if bias is None else (
+            _lib.NSW_EPI_BIAS if residual is None else _lib.NSW_EPI_BIAS_RESIDUAL)
+    eps = default_eps(x.dtype) if eps is None else float(eps)
+    y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=dev)
+    check(lib().nsw_linear_rownorm(x.data_ptr(), w_n.data_ptr(), _p(bias), _p(residual), y.data_ptr(), M, N, K,
+                                   int(epilogue), eps, dtype_code(x), _stream(dev)), "linear_rownorm")
+    return y
+
+
 def window_attention(qkv: torch.Tensor, num_heads: int, scale: float, mask: Optional[torch.Tensor] = None,
                      geometry: Optional[Tuple[int, int, Tuple[int, int], Tuple[int, int], int]] = None
                      ) -> torch.Tensor:
@@ -291,7 +332,7 @@ def swin_block_forward(x: torch.Tensor, packed: dict, num_heads: int, window_siz
     _same_dtype(x, *packed.values())
     hidden = packed["w1"].shape[0]
     shp = block_shape(x, num_heads, window_size, shift_size, hidden, eps)
-    params = _lib.BlockParams(*[packed[n].data_ptr() for n, _ in _lib.BlockParams._fields_])
+    params = _lib.BlockParams(*[_p(packed.get(n)) for n, _ in _lib.BlockParams._fields_])
     nbytes = lib().nsw_block_workspace_size(shp)
     ws = workspace(nbytes, dev)
     y = torch.empty_like(x) if out is None else out

@@ -148,6 +148,12 @@ class Block(nn.Module):
         self._mask_cache = {}
         self._pack_key = None
         self._pack = None
+        # True runs norm1 / norm2 inside the GEMMs that consume them (5
+        # launches per block, row sums of squares from the GEMM's own
+        # fragments).  Off by default: on MI355X the extra VALU work in the
+        # GEMM main loop and the gathered QKV rows cost more than the two
+        # row passes they replace (block 2.14 vs 2.01 ms at 180x360, C=1024).
+        self.fuse_norms = False
 
     # The reference registers attn_mask [nW, T*wa, T*wa] as a non-persistent
     # buffer (models/swin_helpers.py:397).  Here it is materialised on demand
@@ -194,6 +200,14 @@ class Block(nn.Module):
                 "b1": d(self.mlp.bias1.bias), "w2": d(self.mlp.fc2.weight), "b2": d(self.mlp.bias2.bias),
             }
             self._pack_key = key
+        if self.fuse_norms and "wqkv_n1" not in self._pack:
+            # norm weights folded into the GEMM weights that consume the
+            # normalised rows: RMSNorm(x) . W^T = rs(x) * (x . (W * norm_w)^T)
+            with torch.no_grad():
+                pk = self._pack
+                n1, n2 = pk["norm1_w"].float(), pk["norm2_w"].float()
+                pk["wqkv_n1"] = (pk["wqkv"].float() * n1[None, :]).to(pk["wqkv"].dtype).contiguous()
+                pk["w1_n2"] = (pk["w1"].float() * n2[None, :]).to(pk["w1"].dtype).contiguous()
         return self._pack
 
     def _shifted_window_attn(self, x: torch.Tensor) -> torch.Tensor:
@@ -212,7 +226,10 @@ class Block(nn.Module):
         if x.shape[1] != self.temporal_context_window_size:
             raise ValueError("temporal dim does not match temporal_context_window_size")
         self.mlp._check_fusable()
-        return ops.swin_block_forward(x.contiguous(), self.packed(), self.num_heads, self.window_size,
+        pk = self.packed()
+        if not self.fuse_norms:
+            pk = {k: v for k, v in pk.items() if k not in ("wqkv_n1", "w1_n2")}
+        return ops.swin_block_forward(x.contiguous(), pk, self.num_heads, self.window_size,
                                       self.shift_size, eps=self._eps(x.dtype))
 
 
