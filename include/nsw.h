@@ -81,6 +81,14 @@ int nsw_window_reverse_roll(const void* windows, void* x, int64_t B, int64_t T, 
 int nsw_make_attention_mask(float* mask, int64_t H, int64_t W, int64_t ws0, int64_t ws1,
                             int64_t s0, int64_t s1, int64_t T, void* stream);
 
+/* Host-only self-check (no counterpart in the reference): the exact
+ * division by launch constants that the window <-> token row maps use
+ * (roll, partition, reverse, the fused gathers and the proj scatter), tested
+ * against '/' over divisors 1..4096 and large ones at the numerators where an
+ * off-by-one would show.  Returns the number of mismatches (0 = pass); needs
+ * no GPU. */
+int nsw_selftest_fastdiv(void);
+
 /* nn.RMSNorm over the last dim (models/layer_helpers.py:101-119):
  * y = x * rsqrt(mean(x^2) + eps) * w, rows x C. */
 int nsw_rmsnorm(const void* x, const void* w, float eps, void* y, int64_t rows, int64_t C,

@@ -138,16 +138,42 @@ __device__ __forceinline__ float rows4_max(float x) {
   return fmaxf(c, d);
 }
 
+// ------------------------------------------------- division by a constant ---
+// Exact unsigned 32-bit division by a divisor fixed when a kernel is launched
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, Figure 4.1): with l = ceil(log2 d) and
+// mag = floor(2^32 (2^l - d) / d) + 1, every 32-bit n gives
+//   q = (t + ((n - t) >> min(l, 1))) >> max(l - 1, 0),  t = mulhi(mag, n).
+// Five integer instructions instead of a division sequence.
+struct FastDiv {
+  uint32_t mag, sh;   // sh = min(l, 1) | max(l - 1, 0) << 8
+
+  __host__ __device__ static FastDiv make(uint32_t d) {
+    FastDiv f;
+    uint32_t l = 0;
+    while (l < 32 && (1ull << l) < d) ++l;
+    f.mag = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    f.sh = (l < 1 ? l : 1) | ((l > 0 ? l - 1 : 0) << 8);
+    return f;
+  }
+  __host__ __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    const uint32_t t = (uint32_t)(((uint64_t)mag * n) >> 32);
+    return (t + ((n - t) >> (sh & 0xff))) >> (sh >> 8);
+  }
+};
+
 // ------------------------------------------------------- window geometry ----
 // Window-ordered row m of the [B*nW, T*ws0*ws1, C] matrix <-> token of the
 // [B, T, H, W, C] image, with the cyclic shift folded in:
 //   row m = ((b*nW + i*nwb + j)*T + t)*wa + r*ws1 + c
 //   token = ((b*T + t)*H + (i*ws0 + r + s0) mod H)*W + (j*ws1 + c + s1) mod W
 // (roll by -shift, window_partition; the inverse is window_reverse followed by
-//  the roll by +shift).
+//  the roll by +shift).  Rows and tokens are below 2^31 (checked at launch),
+// so the maps run in 32-bit arithmetic with the divisions by constants.
 struct WinGeom {
   int B, T, H, W, ws0, ws1, s0, s1;
   int nhb, nwb, nW, wa, L;  // bands, windows per band, windows per image, ws0*ws1, T*wa
+  FastDiv dL, dwa, dws0, dws1, dnW, dnwb, dHW, dW, dT;
 
   __host__ __device__ static WinGeom make(int B, int T, int H, int W, int ws0, int ws1, int s0, int s1) {
     WinGeom g;
@@ -156,38 +182,43 @@ struct WinGeom {
     g.s0 = ((s0 % H) + H) % H;
     g.s1 = ((s1 % W) + W) % W;
     g.nhb = H / ws0; g.nwb = W / ws1; g.nW = g.nhb * g.nwb; g.wa = ws0 * ws1; g.L = T * g.wa;
+    g.dL = FastDiv::make(g.L); g.dwa = FastDiv::make(g.wa); g.dws0 = FastDiv::make(ws0);
+    g.dws1 = FastDiv::make(ws1); g.dnW = FastDiv::make(g.nW); g.dnwb = FastDiv::make(g.nwb);
+    g.dHW = FastDiv::make((uint32_t)H * (uint32_t)W); g.dW = FastDiv::make(W); g.dT = FastDiv::make(T);
     return g;
   }
 
   __device__ __forceinline__ int64_t token_of_row(int64_t m) const {
-    int64_t win = m / L;
-    int p = (int)(m - win * L);
-    int t = p / wa;
-    int rr = p - t * wa;
-    int r = rr / ws1;
-    int c = rr - r * ws1;
-    int64_t b = win / nW;
-    int wi = (int)(win - b * nW);
-    int i = wi / nwb;
-    int j = wi - i * nwb;
-    int h = i * ws0 + r + s0; if (h >= H) h -= H;
-    int w = j * ws1 + c + s1; if (w >= W) w -= W;
-    return ((b * T + t) * H + h) * (int64_t)W + w;
+    const uint32_t mu = (uint32_t)m;
+    const uint32_t win = dL.div(mu);
+    const uint32_t p = mu - win * (uint32_t)L;
+    const uint32_t t = dwa.div(p);
+    const uint32_t rr = p - t * (uint32_t)wa;
+    const uint32_t r = dws1.div(rr);
+    const uint32_t c = rr - r * (uint32_t)ws1;
+    const uint32_t b = dnW.div(win);
+    const uint32_t wi = win - b * (uint32_t)nW;
+    const uint32_t i = dnwb.div(wi);
+    const uint32_t j = wi - i * (uint32_t)nwb;
+    int h = (int)(i * ws0 + r) + s0; if (h >= H) h -= H;
+    int w = (int)(j * ws1 + c) + s1; if (w >= W) w -= W;
+    return (int64_t)(((b * (uint32_t)T + t) * (uint32_t)H + (uint32_t)h) * (uint32_t)W + (uint32_t)w);
   }
 
   __device__ __forceinline__ int64_t row_of_token(int64_t tok) const {
-    int64_t bt = tok / ((int64_t)H * W);
-    int hw = (int)(tok - bt * (int64_t)H * W);
-    int h = hw / W;
-    int w = hw - h * W;
-    int64_t b = bt / T;
-    int t = (int)(bt - b * T);
-    int hs = h - s0; if (hs < 0) hs += H;
-    int wsft = w - s1; if (wsft < 0) wsft += W;
-    int i = hs / ws0, r = hs - i * ws0;
-    int j = wsft / ws1, c = wsft - j * ws1;
-    int64_t win = b * nW + i * nwb + j;
-    return (win * T + t) * wa + r * ws1 + c;
+    const uint32_t tu = (uint32_t)tok;
+    const uint32_t bt = dHW.div(tu);
+    const uint32_t hw = tu - bt * (uint32_t)H * (uint32_t)W;
+    const uint32_t h = dW.div(hw);
+    const uint32_t w = hw - h * (uint32_t)W;
+    const uint32_t b = dT.div(bt);
+    const uint32_t t = bt - b * (uint32_t)T;
+    int hs = (int)h - s0; if (hs < 0) hs += H;
+    int wsft = (int)w - s1; if (wsft < 0) wsft += W;
+    const uint32_t i = dws0.div((uint32_t)hs), r = (uint32_t)hs - i * (uint32_t)ws0;
+    const uint32_t j = dws1.div((uint32_t)wsft), c = (uint32_t)wsft - j * (uint32_t)ws1;
+    const uint32_t win = b * (uint32_t)nW + i * (uint32_t)nwb + j;
+    return (int64_t)((win * (uint32_t)T + t) * (uint32_t)wa + r * (uint32_t)ws1 + c);
   }
 };
 

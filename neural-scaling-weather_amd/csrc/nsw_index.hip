@@ -22,12 +22,13 @@ __device__ __forceinline__ int64_t src_row(int64_t m, const WinGeom& g) {
     return g.row_of_token(m);          // token <- window-ordered row (roll by +s folded in)
   } else {
     // torch.roll by (s0, s1): y[h, w] = x[(h - s0) mod H, (w - s1) mod W]
-    int64_t bt = m / ((int64_t)g.H * g.W);
-    int hw = (int)(m - bt * (int64_t)g.H * g.W);
-    int h = hw / g.W, w = hw - h * g.W;
-    int hs = h - g.s0; if (hs < 0) hs += g.H;
-    int wsr = w - g.s1; if (wsr < 0) wsr += g.W;
-    return (bt * g.H + hs) * (int64_t)g.W + wsr;
+    const uint32_t mu = (uint32_t)m;
+    const uint32_t bt = g.dHW.div(mu);
+    const uint32_t hw = mu - bt * (uint32_t)g.H * (uint32_t)g.W;
+    const uint32_t h = g.dW.div(hw), w = hw - h * (uint32_t)g.W;
+    int hs = (int)h - g.s0; if (hs < 0) hs += g.H;
+    int wsr = (int)w - g.s1; if (wsr < 0) wsr += g.W;
+    return (int64_t)((bt * (uint32_t)g.H + (uint32_t)hs) * (uint32_t)g.W + (uint32_t)wsr);
   }
 }
 
@@ -122,8 +123,8 @@ int check_geom(int64_t B, int64_t T, int64_t H, int64_t W, int64_t ws0, int64_t 
                 "%s: all of B,T,H,W,ws0,ws1 must be positive", what);
   NSW_CHECK_ARG(H % ws0 == 0 && W % ws1 == 0, "%s: H=%lld, W=%lld not divisible by window (%lld,%lld)",
                 what, (long long)H, (long long)W, (long long)ws0, (long long)ws1);
-  NSW_CHECK_ARG(B * T * H * W < ((int64_t)1 << 40) && H * W < ((int64_t)1 << 31),
-                "%s: image too large", what);
+  NSW_CHECK_ARG(B * T * H * W < ((int64_t)1 << 31), "%s: B*T*H*W=%lld tokens, at most 2^31 - 1", what,
+                (long long)(B * T * H * W));
   return NSW_OK;
 }
 
@@ -147,6 +148,45 @@ __global__ void make_mask_kernel(float* __restrict__ mask, WinGeom g, int64_t to
 }  // namespace nsw
 
 using namespace nsw;
+
+// Host check of FastDiv (the divisions of the row maps) against the '/'
+// operator: every divisor 1..4096 plus large ones, at the numerators where an
+// off-by-one would show (multiples of d and their neighbours, powers of two,
+// the 32-bit extremes) and a pseudo-random sweep.  Returns the failure count.
+extern "C" int nsw_selftest_fastdiv(void) {
+  int fails = 0;
+  auto check = [&](uint32_t d, uint32_t n) {
+    const FastDiv f = FastDiv::make(d);
+    if (f.div(n) != n / d) ++fails;
+  };
+  uint64_t state = 0x9E3779B97F4A7C15ull;
+  auto next = [&]() {
+    state ^= state << 13; state ^= state >> 7; state ^= state << 17;
+    return (uint32_t)(state >> 16);
+  };
+  uint32_t divisors[4096 + 8];
+  int nd = 0;
+  for (uint32_t d = 1; d <= 4096; ++d) divisors[nd++] = d;
+  const uint32_t big[] = {64800u, 259200u, 1036800u, 65535u, 65537u, 2147483647u, 2147483648u, 4294967295u};
+  for (uint32_t d : big) divisors[nd++] = d;
+  for (int a = 0; a < nd; ++a) {
+    const uint32_t d = divisors[a];
+    const uint32_t fixed[] = {0u, 1u, d - 1, d, d + 1, 2 * d - 1, 2 * d, 0x7FFFFFFFu, 0x80000000u,
+                              0xFFFFFFFFu, 0xFFFFFFFEu};
+    for (uint32_t n : fixed) check(d, n);
+    for (int e = 0; e < 32; ++e) { check(d, 1u << e); check(d, (1u << e) - 1); }
+    const uint64_t kmax = 0xFFFFFFFFull / d;
+    for (int s = 0; s < 64; ++s) {
+      const uint64_t k = (uint64_t)next() % (kmax + 1);
+      const uint64_t n = k * d;
+      check(d, (uint32_t)n);
+      if (n > 0) check(d, (uint32_t)(n - 1));
+      if (n + 1 <= 0xFFFFFFFFull) check(d, (uint32_t)(n + 1));
+      check(d, next());
+    }
+  }
+  return fails;
+}
 
 extern "C" int nsw_roll_hw(const void* x, void* y, int64_t B, int64_t T, int64_t H, int64_t W,
                            int64_t C, int64_t s0, int64_t s1, int dtype, void* stream) {

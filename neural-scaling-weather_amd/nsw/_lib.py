@@ -54,6 +54,7 @@ SIGNATURES = {
     "nsw_window_reverse_roll": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                        _int, _vp]),
     "nsw_make_attention_mask": (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "nsw_selftest_fastdiv": (_int, []),
     "nsw_rmsnorm": (_int, [_vp, _vp, _f32, _vp, _i64, _i64, _int, _vp]),
     "nsw_rmsnorm_roll_partition": (_int, [_vp, _vp, _f32, _vp, _i64, _i64, _i64, _i64, _i64,
                                           _i64, _i64, _i64, _i64, _int, _vp]),

@@ -83,6 +83,19 @@ def test_validation_errors_without_gpu(L):
     assert rc == _lib.NSW_ERR_INVALID and b"alias" in L.nsw_last_error()
 
 
+def test_fastdiv_selftest(L):
+    """The exact division by launch constants used by every window <-> token
+    row map matches '/' (host-side check, no GPU)."""
+    assert L.nsw_selftest_fastdiv() == 0
+
+
+def test_token_count_limit(L):
+    from nsw import _lib
+    # the row maps index tokens in 32 bits: 2^31 tokens and more are refused
+    rc = L.nsw_window_partition(16, 16, 1 << 15, 1, 256, 256, 8, 8, 8, _lib.NSW_DTYPE_BF16, None)
+    assert rc == _lib.NSW_ERR_INVALID and b"2^31" in L.nsw_last_error()
+
+
 def test_ops_refuse_cpu_tensors():
     import torch
     from nsw import ops
