@@ -523,15 +523,18 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
     const int prow0 = pass * S::ROWS;                 // first tile row of this pass
     // residual prefetch for this wave's rows of the pass
     u32x4 rres[RES ? ITER : 1];
+    constexpr bool SCAT = EPI == EPI_SCATTER_RESIDUAL;
+    int otok[SCAT ? ITER : 1];                        // output token of each row (scatter), mapped once
     if constexpr (RES) {
 #pragma unroll
       for (int it = 0; it < ITER; ++it) {
         const int rl = (wave * ITER + it) * RPI + lrow;
         const int m = m0 + prow0 + rl;
         rres[it] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (SCAT) otok[it] = m < M ? (int)ea.geom.token_of_row(m) : 0;
         if (m < M && n < N) {
           int64_t orow = m;
-          if constexpr (EPI == EPI_SCATTER_RESIDUAL) orow = ea.geom.token_of_row(m);
+          if constexpr (SCAT) orow = otok[it];
           rres[it] = *reinterpret_cast<const u32x4*>((const T*)ea.residual + orow * N + n);
         }
       }
@@ -554,7 +557,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
       const int m = m0 + prow0 + rl;
       if (m < M && n < N) {
         int64_t orow = m;
-        if constexpr (EPI == EPI_SCATTER_RESIDUAL) orow = ea.geom.token_of_row(m);
+        if constexpr (SCAT) orow = otok[it];
         float o[VEC];
         load16<T>(reinterpret_cast<const T*>(stg + rl * S::STRIDE) + col, o);
         if constexpr (RES) {
