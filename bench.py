@@ -78,9 +78,10 @@ def main():
     ap.add_argument("--no-model", action="store_true", help="skip the config-3 forecast and config-5 rollout")
     ap.add_argument("--model-steps", type=int, default=10, help="timed forecast steps (config 3)")
     ap.add_argument("--no-rollout", action="store_true", help="skip the config-5 rollout")
-    ap.add_argument("--fused-norms", action="store_true",
-                    help="fold the block's two RMSNorms into the GEMMs that consume them (5 launches "
-                         "instead of 7; slower on MI355X, kept as an ablation)")
+    ap.add_argument("--norms", choices=["fold2", "fold12", "separate"], default="fold2",
+                    help="fold2 (default): norm2 folded into proj/fc1 via row sums of squares, 6 launches; "
+                         "fold12: norm1 also folded into the QKV GEMM, 5 launches (slower, an ablation); "
+                         "separate: both norms as passes of their own, 7 launches")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (5 launches): the reference kernel whose "
@@ -113,7 +114,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.manual_seed(1001)
     blk = nsw.Block(C, heads, (H, W), ws, T, shift_size=shift).to(device=dev, dtype=dtype).eval()
-    blk.fuse_norms = args.fused_norms
+    blk.fold_norm1 = args.norms == "fold12"
+    blk.fold_norm2 = args.norms != "separate"
     g = torch.Generator().manual_seed(1002)
     x = torch.randn(B, T, H, W, C, generator=g).to(device=dev, dtype=dtype)
     M = B * T * H * W
@@ -142,47 +144,59 @@ def main():
         # them on the launch stream
         pk = blk.packed()
         eps = blk._eps(dtype)
-        if blk.fuse_norms:
-            names = ["qkv_norm_gather", "attention", "proj_scatter", "fc1_rownorm", "fc2"]
-        else:
-            names = ["gather_norm1", "qkv", "attention", "proj_scatter", "norm2", "fc1", "fc2"]
+        scale = (C // heads) ** -0.5
+        st = {}
+
+        def k_gather():
+            st["xw"] = ops.rmsnorm_roll_partition(x, pk["norm1_w"], ws, shift, eps)
+
+        def k_qkv():
+            st["qkv"] = ops.qkv_projection(st["xw"], pk["wqkv"], pk["bqkv"], pk["qn_w"], pk["kn_w"], heads, eps)
+
+        def k_qkv_ng():
+            st["qkv"] = ops.qkv_projection_norm_gather(x, pk["wqkv_n1"], pk["bqkv"], pk["qn_w"], pk["kn_w"], heads,
+                                                       ws, shift, eps)
+
+        def k_attn():
+            st["o"] = ops.window_attention(st["qkv"], heads, scale, geometry=(H, W, ws, shift, T))
+
+        def k_proj():
+            st["h1"] = ops.proj_reverse_residual(st["o"], pk["wproj"], pk["bproj"], x, ws, shift)
+
+        def k_proj_ss():
+            st["h1"], st["ss"] = ops.proj_reverse_residual_sumsq(st["o"], pk["wproj"], pk["bproj"], x, ws, shift)
+
+        def k_norm2():
+            st["hn"] = ops.rms_norm(st["h1"], pk["norm2_w"], eps)
+
+        def k_fc1():
+            st["u"] = ops.linear(st["hn"], pk["w1"], pk["b1"], epilogue=_lib.NSW_EPI_BIAS_GELU)
+
+        def k_fc1_rs():
+            st["u"] = ops.linear_rowscale(st["h1"], pk["w1_n2"], st["ss"], pk["b1"],
+                                          epilogue=_lib.NSW_EPI_BIAS_GELU, eps=eps)
+
+        def k_fc2():
+            st["y"] = ops.linear(st["u"], pk["w2"], pk["b2"], residual=st["h1"])
+
+        seq = ([("qkv_norm_gather", k_qkv_ng)] if blk.fold_norm1 else [("gather_norm1", k_gather), ("qkv", k_qkv)])
+        seq += [("attention", k_attn)]
+        seq += ([("proj_scatter_sumsq", k_proj_ss), ("fc1_rowscale", k_fc1_rs)] if blk.fold_norm2 else
+                [("proj_scatter", k_proj), ("norm2", k_norm2), ("fc1", k_fc1)])
+        seq += [("fc2", k_fc2)]
+        names = [n for n, _ in seq]
         times = {n: [] for n in names}
         for it in range(args.warmup + args.steps):
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
-            k = 0
-            ev[k].record(stream)
-            if blk.fuse_norms:
-                qkv = ops.qkv_projection_norm_gather(x, pk["wqkv_n1"], pk["bqkv"], pk["qn_w"], pk["kn_w"],
-                                                     heads, ws, shift, eps)
-            else:
-                xw = ops.rmsnorm_roll_partition(x, pk["norm1_w"], ws, shift, eps)
-                k += 1
-                ev[k].record(stream)
-                qkv = ops.qkv_projection(xw, pk["wqkv"], pk["bqkv"], pk["qn_w"], pk["kn_w"], heads, eps)
-            k += 1
-            ev[k].record(stream)
-            o = ops.window_attention(qkv, heads, (C // heads) ** -0.5, geometry=(H, W, ws, shift, T))
-            k += 1
-            ev[k].record(stream)
-            h1 = ops.proj_reverse_residual(o, pk["wproj"], pk["bproj"], x, ws, shift)
-            k += 1
-            ev[k].record(stream)
-            if blk.fuse_norms:
-                u = ops.linear_rownorm(h1, pk["w1_n2"], pk["b1"], epilogue=_lib.NSW_EPI_BIAS_GELU, eps=eps)
-            else:
-                hn = ops.rms_norm(h1, pk["norm2_w"], eps)
-                k += 1
-                ev[k].record(stream)
-                u = ops.linear(hn, pk["w1"], pk["b1"], epilogue=_lib.NSW_EPI_BIAS_GELU)
-            k += 1
-            ev[k].record(stream)
-            y2 = ops.linear(u, pk["w2"], pk["b2"], residual=h1)
-            k += 1
-            ev[k].record(stream)
+            ev[0].record(stream)
+            for i, (_, fn) in enumerate(seq):
+                fn()
+                ev[i + 1].record(stream)
             torch.cuda.synchronize()
             if it >= args.warmup:
                 for i, n in enumerate(names):
                     times[n].append(ev[i].elapsed_time(ev[i + 1]))
+        y2 = st["y"]
         same = torch.equal(y2, y)
 
     es = 2 if dtype == torch.bfloat16 else 4
@@ -192,7 +206,8 @@ def main():
     work = {  # (algorithmic units per launch, bound)
         "gather_norm1": (2 * A, "hbm"), "qkv": (fl["qkv"], "mfma"), "attention": (4 * A, "hbm"),
         "proj_scatter": (fl["proj"], "mfma"), "norm2": (2 * A, "hbm"), "fc1": (fl["fc1"], "mfma"),
-        "fc2": (fl["fc2"], "mfma"), "qkv_norm_gather": (fl["qkv"], "mfma"), "fc1_rownorm": (fl["fc1"], "mfma"),
+        "fc2": (fl["fc2"], "mfma"), "qkv_norm_gather": (fl["qkv"], "mfma"), "fc1_rowscale": (fl["fc1"], "mfma"),
+        "proj_scatter_sumsq": (fl["proj"], "mfma"),
     }
     kern = {}
     for n in names:
@@ -234,14 +249,14 @@ def main():
         "config": {"workload": desc, "tokens": M, "block_tflop": round(total_flops / 1e12, 4),
                    "block_tflops_achieved": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
                    "wall_s_timed": round(wall, 4), "ops_path_equals_fused": bool(same),
-                   "block_launches": len(names)},
+                   "block_launches": len(names), "norms": args.norms},
         "roofline": roofline,
         "kernels": kern,
     }
 
     # ------------------------------------------------- config 3 / config 5
     if not args.no_model:
-        del y, y2, qkv, o, h1, u
+        del y, y2, st
         torch.cuda.empty_cache()
         out["forecast"], rollout = model_sections(dev, args.model_steps, args.warmup, not args.no_rollout)
         if rollout is not None:

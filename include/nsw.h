@@ -136,6 +136,22 @@ int nsw_proj_reverse_residual(const void* o, const void* wproj, const void* bpro
                               int64_t W, int64_t C, int64_t ws0, int64_t ws1, int64_t s0,
                               int64_t s1, int dtype, void* stream);
 
+/* Number of partial sums per row that nsw_proj_reverse_residual_sumsq writes
+ * for rows of C elements: one per 256 bytes of row, ceil(C * esize / 256). */
+int64_t nsw_row_sumsq_parts(int64_t C, int dtype);
+
+/* nsw_proj_reverse_residual that also writes, for each output row (token t),
+ * partial sums of the squares of the values it stores (after the residual,
+ * in the output dtype): row_sumsq[t * P + p] = sum of y[t, c]^2 over the p-th
+ * 256-byte segment of the row, P = nsw_row_sumsq_parts(C, dtype), fp32.
+ * These are the statistics of Block.forward's norm2 (models/swin_helpers.py
+ * :457, nn.RMSNorm over h1), so that the consumer GEMM (nsw_linear_rowscale)
+ * normalises h1 without a separate pass over it. */
+int nsw_proj_reverse_residual_sumsq(const void* o, const void* wproj, const void* bproj,
+                                    const void* skip, void* y, float* row_sumsq, int64_t B,
+                                    int64_t T, int64_t H, int64_t W, int64_t C, int64_t ws0,
+                                    int64_t ws1, int64_t s0, int64_t s1, int dtype, void* stream);
+
 /* Whole Block.forward (models/swin_helpers.py:435-459). */
 typedef struct nsw_block_params {
   const void* norm1_w;   /* [C]          norm1.norm.weight                      */
@@ -150,13 +166,12 @@ typedef struct nsw_block_params {
   const void* b1;        /* [Hm]         mlp.bias1.bias                         */
   const void* w2;        /* [C, Hm]      mlp.fc2.weight                         */
   const void* b2;        /* [C]          mlp.bias2.bias                         */
-  /* Optional norm-folded weights (both or neither): wqkv_n1[n,k] =
-   * wqkv[n,k] * norm1_w[k], w1_n2[n,k] = w1[n,k] * norm2_w[k].  When given,
-   * the two RMSNorms run inside the GEMMs that consume them (5 launches:
-   * nsw_qkv_projection_norm_gather, attention, proj scatter,
-   * nsw_linear_rownorm, fc2) instead of as separate passes (7 launches).
-   * The 7-launch form is the faster one on MI355X (the row sums add VALU work
-   * to the GEMM main loop); the folded form is kept as an option. */
+  /* Optional norm-folded weights: w1_n2[n,k] = w1[n,k] * norm2_w[k] removes
+   * the norm2 pass (the proj GEMM writes h1's row sums of squares, fc1 applies
+   * the row scale: 6 launches, the faster form); wqkv_n1[n,k] = wqkv[n,k] *
+   * norm1_w[k] also folds norm1 into the QKV GEMM (5 launches; that GEMM
+   * then gathers token rows and sums their squares itself, which measured
+   * slower on MI355X than the separate norm1 gather). */
   const void* wqkv_n1;   /* [3C, C] or NULL                                     */
   const void* w1_n2;     /* [Hm, C] or NULL                                     */
 } nsw_block_params;
@@ -226,6 +241,16 @@ int nsw_qkv_projection_norm_gather(const void* x, const void* wqkv_n, const void
 int nsw_linear_rownorm(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
                        int64_t M, int64_t N, int64_t K, int epilogue, float eps, int dtype,
                        void* stream);
+
+/* y = epi(RMSNorm(x; norm_w, eps) . W^T) (norm2 + MLP fc1, models/swin_helpers.py
+ * :457, models/mlp.py:80-85) with the row statistics supplied by x's producer:
+ * w_n[n,k] = W[n,k] * norm_w[k], rs[m] = 1/sqrt(sum_p row_sumsq[m*nparts + p] / K
+ * + eps) applied to each row of x . w_n^T before the bias.  row_sumsq as
+ * written by nsw_proj_reverse_residual_sumsq.  Epilogues and requirements as
+ * nsw_linear. */
+int nsw_linear_rowscale(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
+                        const float* row_sumsq, int64_t nparts, int64_t M, int64_t N, int64_t K,
+                        int epilogue, float eps, int dtype, void* stream);
 
 /* Patch matrix of the stride-p patch convolution (PatchEmbedLayer,
  * models/layer_helpers.py:120-172, as called by SwinTransformer.prepare_tokens,

@@ -8,17 +8,23 @@
 //   K6  u   = gelu(hn . W1^T + b1)                                 (MFMA GEMM)
 //   K7  y   = u . W2^T + b2 + h1                                   (MFMA GEMM)
 //
-// With the norm-folded weights (p->wqkv_n1, p->w1_n2) K1 and K5 disappear
-// into the GEMMs that consume them:
+// With the norm-folded weight w1_n2 = W1 * norm2 (per input column), K5
+// disappears: K4 also writes partial sums of squares of the h1 rows it
+// stores (S, [M, nparts]) and
 //
-//   K2' qkv = per-head-norm(rs1 . (gather(x) . (Wqkv*norm1)^T) + b)
-//   K6' u   = gelu(rs2 . (h1 . (W1*norm2)^T) + b1)
+//   K6' u   = gelu(rs2 . (h1 . w1_n2^T) + b1),  rs2 = 1/sqrt(sum(S row) / C + eps)
 //
-// with rs the rows' 1/sqrt(mean square + eps), accumulated from the GEMMs'
-// own x / h1 fragments (5 launches).
+// (6 launches, the default of nsw.Block).  With wqkv_n1 = Wqkv * norm1 as
+// well, K1 folds into the QKV GEMM, which gathers the token rows and
+// accumulates their sums of squares from its own fragments:
 //
-// Workspace (dtype elements): A [M*C] holds xw, then o, then hn; Q [M*max(3C,
-// Hm)] holds qkv, then u; H1 [M*C] holds h1.  M = B*T*H*W tokens.
+//   K2' qkv = per-head-norm(rs1 . (gather(x) . wqkv_n1^T) + b)
+//
+// (5 launches; measured slower than K1 + K2 on MI355X, kept as an option).
+//
+// Workspace: A [M*C] holds xw, then o, then hn; Q [M*max(3C, Hm)] holds qkv,
+// then u; H1 [M*C] holds h1 (dtype elements); S [M*nparts] float.
+// M = B*T*H*W tokens.
 #include "nsw_common.h"
 
 namespace nsw {
@@ -26,18 +32,20 @@ int gemm_qkv(const void* x, const void* wqkv, const void* bqkv, const void* qn_w
              float eps, void* qkv, int64_t M, int64_t C, int64_t num_heads, int dtype, void* stream);
 int gemm_proj_scatter(const void* o, const void* wproj, const void* bproj, const void* skip, void* y,
                       int64_t B, int64_t T, int64_t H, int64_t W, int64_t C, int64_t ws0, int64_t ws1,
-                      int64_t s0, int64_t s1, int dtype, void* stream);
+                      int64_t s0, int64_t s1, int dtype, void* stream, float* row_sumsq);
+int gemm_linear_rowscale(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
+                         const float* row_sumsq, int64_t nparts, int64_t M, int64_t N, int64_t K, int epilogue,
+                         float eps, int dtype, void* stream);
+int64_t sumsq_parts(int64_t C, int dtype);
 int gemm_qkv_norm_gather(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w,
                          const void* kn_w, float eps, void* qkv, int64_t B, int64_t T, int64_t H, int64_t W,
                          int64_t C, int64_t num_heads, int64_t ws0, int64_t ws1, int64_t s0, int64_t s1,
                          int dtype, void* stream);
-int gemm_linear_rownorm(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
-                        int64_t M, int64_t N, int64_t K, int epilogue, float eps, int dtype, void* stream);
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct BlockLayout {
-  size_t a, q, h1, total;
+  size_t a, q, h1, ss, total;
 };
 
 static BlockLayout block_layout(const nsw_block_shape* s) {
@@ -49,7 +57,8 @@ static BlockLayout block_layout(const nsw_block_shape* s) {
   l.a = 0;
   l.q = align256(M * C * es);
   l.h1 = l.q + align256(M * wq * es);
-  l.total = l.h1 + align256(M * C * es);
+  l.ss = l.h1 + align256(M * C * es);
+  l.total = l.ss + align256(M * (size_t)sumsq_parts(s->C, s->dtype) * sizeof(float));
   return l;
 }
 }  // namespace nsw
@@ -80,50 +89,44 @@ extern "C" int nsw_swin_block_forward(const void* x, void* y, const nsw_block_pa
   const int64_t C = s->C;
   const int64_t L = s->T * s->ws0 * s->ws1;
   const int64_t hd = C / s->num_heads;
+  float* S = (float*)(ws + lay.ss);
+  const int64_t nparts = sumsq_parts(C, s->dtype);
   int rc;
-  NSW_CHECK_ARG((p->wqkv_n1 == nullptr) == (p->w1_n2 == nullptr), "%s: give both norm-folded weights or neither",
-                what);
   if (p->wqkv_n1) {
     // K2'
     rc = gemm_qkv_norm_gather(x, p->wqkv_n1, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, s->B, s->T, s->H, s->W, C,
                               s->num_heads, s->ws0, s->ws1, s->s0, s->s1, s->dtype, stream);
     if (rc) return rc;
-    // K3
-    rc = nsw_window_attention(Q, A, nullptr, 0, M / L, L, C, s->num_heads, 1.0f / sqrtf((float)hd), s->H,
-                              s->W, s->ws0, s->ws1, s->s0, s->s1, s->T, s->dtype, stream);
+  } else {
+    // K1
+    rc = nsw_rmsnorm_roll_partition(x, p->norm1_w, s->eps, A, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1,
+                                    s->s0, s->s1, s->dtype, stream);
     if (rc) return rc;
-    // K4
-    rc = gemm_proj_scatter(A, p->wproj, p->bproj, x, H1, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1, s->s0,
-                           s->s1, s->dtype, stream);
+    // K2
+    rc = gemm_qkv(A, p->wqkv, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, M, C, s->num_heads, s->dtype, stream);
     if (rc) return rc;
-    // K6' (u overwrites qkv in Q)
-    rc = gemm_linear_rownorm(H1, p->w1_n2, p->b1, nullptr, Q, M, s->hidden, C, NSW_EPI_BIAS_GELU, s->eps,
-                             s->dtype, stream);
-    if (rc) return rc;
-    // K7
-    return nsw_linear(Q, p->w2, p->b2, H1, y, M, C, s->hidden, NSW_EPI_BIAS_RESIDUAL, s->dtype, stream);
   }
-  // K1
-  rc = nsw_rmsnorm_roll_partition(x, p->norm1_w, s->eps, A, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1,
-                                  s->s0, s->s1, s->dtype, stream);
-  if (rc) return rc;
-  // K2
-  rc = gemm_qkv(A, p->wqkv, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, M, C, s->num_heads, s->dtype, stream);
-  if (rc) return rc;
   // K3 (o overwrites xw in A)
   rc = nsw_window_attention(Q, A, nullptr, 0, M / L, L, C, s->num_heads, 1.0f / sqrtf((float)hd), s->H,
                             s->W, s->ws0, s->ws1, s->s0, s->s1, s->T, s->dtype, stream);
   if (rc) return rc;
-  // K4
+  // K4 (+ the row partial sums of squares of h1 when norm2 is folded)
   rc = gemm_proj_scatter(A, p->wproj, p->bproj, x, H1, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1, s->s0,
-                         s->s1, s->dtype, stream);
+                         s->s1, s->dtype, stream, p->w1_n2 ? S : nullptr);
   if (rc) return rc;
-  // K5 (hn overwrites o in A)
-  rc = nsw_rmsnorm(H1, p->norm2_w, s->eps, A, M, C, s->dtype, stream);
-  if (rc) return rc;
-  // K6 (u overwrites qkv in Q)
-  rc = nsw_linear(A, p->w1, p->b1, nullptr, Q, M, s->hidden, C, NSW_EPI_BIAS_GELU, s->dtype, stream);
-  if (rc) return rc;
+  if (p->w1_n2) {
+    // K6' (u overwrites qkv in Q)
+    rc = gemm_linear_rowscale(H1, p->w1_n2, p->b1, nullptr, Q, S, nparts, M, s->hidden, C, NSW_EPI_BIAS_GELU,
+                              s->eps, s->dtype, stream);
+    if (rc) return rc;
+  } else {
+    // K5 (hn overwrites o in A)
+    rc = nsw_rmsnorm(H1, p->norm2_w, s->eps, A, M, C, s->dtype, stream);
+    if (rc) return rc;
+    // K6 (u overwrites qkv in Q)
+    rc = nsw_linear(A, p->w1, p->b1, nullptr, Q, M, s->hidden, C, NSW_EPI_BIAS_GELU, s->dtype, stream);
+    if (rc) return rc;
+  }
   // K7
   rc = nsw_linear(Q, p->w2, p->b2, H1, y, M, C, s->hidden, NSW_EPI_BIAS_RESIDUAL, s->dtype, stream);
   return rc;

@@ -129,6 +129,16 @@ __device__ __forceinline__ float rows4_sum(float x) {
   return c + d;
 }
 
+// Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), on every lane:
+// rotations by 8, 4, 2, 1 within the row.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x122, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x121, 0xf, 0xf, false));
+  return x;
+}
+
 __device__ __forceinline__ float rows4_max(float x) {
   float a = x, b = x;
   permlane16_swap(a, b);

@@ -72,7 +72,12 @@ enum Epi {
 //   PRE_ROWNORM_GATHER  as PRE_ROWNORM, and the copy of x row m reads token
 //                row token_of_row(m) of the image (roll by -shift + window
 //                partition folded into the copy addresses).
-enum Pre { PRE_NONE = 0, PRE_ROWNORM = 1, PRE_ROWNORM_GATHER = 2 };
+//   PRE_ROWSCALE y = epi(rs . (x . w^T)) with rs[m] = 1/sqrt(sum_p P[m,p] / K + eps)
+//                from per-row partial sums of squares P [M, nparts] written by
+//                the producer of x (the proj scatter epilogue): the norm costs
+//                the consumer one read per row instead of a pass over x.
+enum Pre { PRE_NONE = 0, PRE_ROWNORM = 1, PRE_ROWNORM_GATHER = 2, PRE_ROWSCALE = 3 };
+constexpr bool pre_sums_in_loop(int pre) { return pre == PRE_ROWNORM || pre == PRE_ROWNORM_GATHER; }
 
 constexpr int qkv_head_dim(int epi) {
   return (epi == EPI_QKV_HN16 || epi == EPI_QKV_HN32 || epi == EPI_QKV_HN64) ? epi : 0;
@@ -129,6 +134,8 @@ struct EpiArgs {
   float eps;
   int C;       // q/k/v width for the QKV epilogues
   WinGeom geom;  // EPI_SCATTER_RESIDUAL
+  float* row_sumsq;   // scatter epilogue: optional [tokens, nparts] output; PRE_ROWSCALE: input
+  int nparts;
 };
 
 // GELU with the exact-erf form of nn.GELU(): 0.5 v (1 + erf(v / sqrt 2)).
@@ -386,7 +393,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
         if (mb < NB) fa[(U + 1) & 1][mb] = lds_frag<ROWB>(nx, arow + mb * 16, nch_ + fg);      \
         _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                      \
           mfma_chunk<T>(acc[nb][mb], fa[U & 1][nb], fb[U & 1][mb]);                            \
-        if constexpr (PRE != PRE_NONE) ssr[mb] = frag_sumsq<T>(fb[U & 1][mb], ssr[mb]);        \
+        if constexpr (pre_sums_in_loop(PRE)) ssr[mb] = frag_sumsq<T>(fb[U & 1][mb], ssr[mb]);  \
         if (mb < NB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                        \
         else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                \
         __builtin_amdgcn_sched_group_barrier(0x008, NB * (sizeof(T) == 2 ? 1 : 4), 0);         \
@@ -424,9 +431,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
     const int n = nw0 + nb * 16 + fg * 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) bv[nb][r] = 0.f;
-    if constexpr (EPI != EPI_NONE) {
-      if (n < N) load4<T>(bias + n, bv[nb]);
-    }
+    if constexpr (EPI != EPI_NONE) load4<T>(bias + (n < N ? n : 0), bv[nb]);   // straight-line: one batch
   }
 
   // per-head RMSNorm (QKV epilogue): a head is HDQ/16 consecutive 16-column
@@ -445,8 +450,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
       normed[h] = region < 2 && c0 < N;
       const T* nwp = (const T*)(region == 0 ? ea.qn_w : ea.kn_w);
 #pragma unroll
-      for (int b = 0; b < NBH; ++b)
-        if (normed[h]) load4<T>(nwp + b * 16 + fg * 4, nwv[h * NBH + b]);
+      for (int b = 0; b < NBH; ++b) load4<T>(nwp + b * 16 + fg * 4, nwv[h * NBH + b]);   // used only if normed
     }
   }
 
@@ -455,7 +459,38 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     rsr[mb] = 1.f;
-    if constexpr (PRE != PRE_NONE) rsr[mb] = 1.0f / sqrtf(rows4_sum(ssr[mb]) / (float)K + ea.eps);
+    if constexpr (pre_sums_in_loop(PRE)) rsr[mb] = 1.0f / sqrtf(rows4_sum(ssr[mb]) / (float)K + ea.eps);
+  }
+  if constexpr (PRE == PRE_ROWSCALE) {
+    // the producer's partial sums of this lane's MB x rows, read as one batch
+    // of loads per 4 partials (rows past M read row 0 and are never stored)
+    const float* pp[MB];
+    float ss[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = m0 + wm * WTM + mb * 16 + frow;
+      pp[mb] = ea.row_sumsq + (int64_t)(m < M ? m : 0) * ea.nparts;
+      ss[mb] = 0.f;
+    }
+    int q = 0;
+    if ((ea.nparts & 3) == 0) {
+      for (; q < ea.nparts; q += 4) {
+        f32x4 v[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) v[mb] = *reinterpret_cast<const f32x4*>(pp[mb] + q);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) ss[mb] += (v[mb][0] + v[mb][1]) + (v[mb][2] + v[mb][3]);
+      }
+    }
+    for (; q < ea.nparts; ++q) {
+      float v[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) v[mb] = pp[mb][q];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) ss[mb] += v[mb];
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) rsr[mb] = 1.0f / sqrtf(ss[mb] / (float)K + ea.eps);
   }
 
   // 1. epilogue math in the fragment layout, in place
@@ -555,6 +590,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
     for (int it = 0; it < ITER; ++it) {
       const int rl = (wave * ITER + it) * RPI + lrow;
       const int m = m0 + prow0 + rl;
+      float ssq = 0.f;                                // sum of squares of this lane's stored values
       if (m < M && n < N) {
         int64_t orow = m;
         if constexpr (SCAT) orow = otok[it];
@@ -575,6 +611,22 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
           for (int e = 0; e < VEC; ++e) o[e] += rv[e];
         }
         store16<T>(Y + orow * N + n, o);
+        if constexpr (SCAT) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const float r = sizeof(T) == 2 ? (float)(T)o[e] : o[e];   // the stored value
+            ssq = fmaf(r, r, ssq);
+          }
+        }
+      }
+      if constexpr (SCAT) {
+        // partial sum of squares over the 16 lanes (16 * VEC columns) of a
+        // DPP row, one float per 256 bytes of output row
+        if (ea.row_sumsq != nullptr) {
+          ssq = row16_sum(ssq);
+          if ((lane & 15) == 0 && m < M && n < N)
+            ea.row_sumsq[(int64_t)otok[it] * ea.nparts + n / (16 * VEC)] = ssq;
+        }
       }
     }
     if (pass + 1 < S::PASSES) wg_barrier();          // before the next pass overwrites the staging rows
@@ -640,10 +692,17 @@ int gemm_qkv(const void* x, const void* wqkv, const void* bqkv, const void* qn_w
   return dispatch_gemm<EPI_QKV_HN16>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
 }
 
+// Partial sums of squares per output row: one float per 256 bytes of row
+// (16 lanes of 16-byte stores in the scatter epilogue).
+int64_t sumsq_parts(int64_t C, int dtype) {
+  const int64_t es = dtype == NSW_DTYPE_F32 ? 4 : 2;
+  return (C * es + 255) / 256;
+}
+
 int gemm_proj_scatter(const void* o, const void* wproj, const void* bproj, const void* skip, void* y,
                       int64_t B, int64_t T, int64_t H, int64_t W, int64_t C, int64_t ws0, int64_t ws1,
-                      int64_t s0, int64_t s1, int dtype, void* stream) {
-  const char* what = "nsw_proj_reverse_residual";
+                      int64_t s0, int64_t s1, int dtype, void* stream, float* row_sumsq) {
+  const char* what = row_sumsq ? "nsw_proj_reverse_residual_sumsq" : "nsw_proj_reverse_residual";
   int rc = check_geom(B, T, H, W, ws0, ws1, what);
   if (rc) return rc;
   NSW_CHECK_ARG(bproj && skip, "%s: bias and skip are required", what);
@@ -651,7 +710,35 @@ int gemm_proj_scatter(const void* o, const void* wproj, const void* bproj, const
   EpiArgs ea{};
   ea.bias = bproj; ea.residual = skip;
   ea.geom = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
+  ea.row_sumsq = row_sumsq;
+  ea.nparts = (int)sumsq_parts(C, dtype);
   return dispatch_gemm<EPI_SCATTER_RESIDUAL>(dtype, o, wproj, y, B * T * H * W, C, C, ea, stream, what);
+}
+
+// y = epi(rs . (x . w_n^T)), rs[m] = 1/sqrt(sum_p row_sumsq[m, p] / K + eps):
+// RMSNorm(x) folded into the GEMM with the row statistics from x's producer.
+int gemm_linear_rowscale(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
+                         const float* row_sumsq, int64_t nparts, int64_t M, int64_t N, int64_t K, int epilogue,
+                         float eps, int dtype, void* stream) {
+  const char* what = "nsw_linear_rowscale";
+  NSW_CHECK_ARG(row_sumsq != nullptr && nparts > 0 && nparts <= 4096, "%s: row_sumsq [M, nparts] is required",
+                what);
+  NSW_CHECK_ARG(((uintptr_t)row_sumsq % 16) == 0, "%s: row_sumsq must be 16-byte aligned", what);
+  EpiArgs ea{};
+  ea.bias = bias; ea.residual = residual; ea.eps = eps;
+  ea.row_sumsq = const_cast<float*>(row_sumsq);
+  ea.nparts = (int)nparts;
+  if (epilogue != NSW_EPI_NONE) NSW_CHECK_ARG(bias != nullptr, "%s: epilogue %d needs a bias", what, epilogue);
+  switch (epilogue) {
+    case NSW_EPI_NONE: return dispatch_gemm<EPI_NONE, PRE_ROWSCALE>(dtype, x, w_n, y, M, N, K, ea, stream, what);
+    case NSW_EPI_BIAS: return dispatch_gemm<EPI_BIAS, PRE_ROWSCALE>(dtype, x, w_n, y, M, N, K, ea, stream, what);
+    case NSW_EPI_BIAS_GELU:
+      return dispatch_gemm<EPI_BIAS_GELU, PRE_ROWSCALE>(dtype, x, w_n, y, M, N, K, ea, stream, what);
+    case NSW_EPI_BIAS_RESIDUAL:
+      NSW_CHECK_ARG(residual != nullptr, "%s: residual epilogue needs a residual", what);
+      return dispatch_gemm<EPI_BIAS_RESIDUAL, PRE_ROWSCALE>(dtype, x, w_n, y, M, N, K, ea, stream, what);
+    default: return set_error(NSW_ERR_INVALID, "%s: unknown epilogue %d", what, epilogue);
+  }
 }
 
 // QKV projection of RMSNorm(x) gathered into window order: qkv[m] =
@@ -748,5 +835,21 @@ extern "C" int nsw_proj_reverse_residual(const void* o, const void* wproj, const
                                          const void* skip, void* y, int64_t B, int64_t T, int64_t H,
                                          int64_t W, int64_t C, int64_t ws0, int64_t ws1, int64_t s0,
                                          int64_t s1, int dtype, void* stream) {
-  return gemm_proj_scatter(o, wproj, bproj, skip, y, B, T, H, W, C, ws0, ws1, s0, s1, dtype, stream);
+  return gemm_proj_scatter(o, wproj, bproj, skip, y, B, T, H, W, C, ws0, ws1, s0, s1, dtype, stream, nullptr);
+}
+
+extern "C" int64_t nsw_row_sumsq_parts(int64_t C, int dtype) { return C > 0 ? sumsq_parts(C, dtype) : 0; }
+
+extern "C" int nsw_proj_reverse_residual_sumsq(const void* o, const void* wproj, const void* bproj,
+                                               const void* skip, void* y, float* row_sumsq, int64_t B,
+                                               int64_t T, int64_t H, int64_t W, int64_t C, int64_t ws0,
+                                               int64_t ws1, int64_t s0, int64_t s1, int dtype, void* stream) {
+  NSW_CHECK_ARG(row_sumsq != nullptr, "nsw_proj_reverse_residual_sumsq: row_sumsq is required");
+  return gemm_proj_scatter(o, wproj, bproj, skip, y, B, T, H, W, C, ws0, ws1, s0, s1, dtype, stream, row_sumsq);
+}
+
+extern "C" int nsw_linear_rowscale(const void* x, const void* w_n, const void* bias, const void* residual,
+                                   void* y, const float* row_sumsq, int64_t nparts, int64_t M, int64_t N,
+                                   int64_t K, int epilogue, float eps, int dtype, void* stream) {
+  return gemm_linear_rowscale(x, w_n, bias, residual, y, row_sumsq, nparts, M, N, K, epilogue, eps, dtype, stream);
 }

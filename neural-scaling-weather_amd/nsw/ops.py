@@ -298,6 +298,51 @@ def proj_reverse_residual(o: torch.Tensor, wproj: torch.Tensor, bproj: torch.Ten
     return y
 
 
+def proj_reverse_residual_sumsq(o: torch.Tensor, wproj: torch.Tensor, bproj: torch.Tensor, skip: torch.Tensor,
+                                window_size, shift_size):
+    """proj_reverse_residual that also returns the partial sums of squares of
+    each output row [B*T*H*W, P] (fp32, one per 256 bytes of row), the
+    statistics of the RMSNorm that follows."""
+    B, T, H, W, C = skip.shape
+    dev = _dev(o, wproj, bproj, skip)
+    _same_dtype(o, wproj, bproj, skip)
+    y = torch.empty_like(skip)
+    P = int(lib().nsw_row_sumsq_parts(C, dtype_code(skip)))
+    ss = torch.empty(B * T * H * W, P, dtype=torch.float32, device=dev)
+    check(lib().nsw_proj_reverse_residual_sumsq(o.data_ptr(), wproj.data_ptr(), bproj.data_ptr(),
+                                                skip.data_ptr(), y.data_ptr(), ss.data_ptr(), B, T, H, W, C,
+                                                window_size[0], window_size[1], int(shift_size[0]),
+                                                int(shift_size[1]), dtype_code(o), _stream(dev)),
+          "proj_reverse_residual_sumsq")
+    return y, ss
+
+
+def linear_rowscale(x: torch.Tensor, w_n: torch.Tensor, row_sumsq: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                    residual: Optional[torch.Tensor] = None, epilogue: Optional[int] = None,
+                    eps: Optional[float] = None) -> torch.Tensor:
+    """y = epi(RMSNorm(x) . W^T) with w_n = W * norm_w and the rows' sums of
+    squares given as partials row_sumsq [M, P] (from proj_reverse_residual_sumsq)."""
+    dev = _dev(x, w_n, bias, residual, row_sumsq)
+    _same_dtype(x, w_n, bias, residual)
+    K = x.shape[-1]
+    N, Kw = w_n.shape
+    if Kw != K:
+        raise ValueError(f"linear_rowscale: x has {K} features, weight expects {Kw}")
+    M = x.numel() // K
+    if row_sumsq.dtype != torch.float32 or row_sumsq.dim() != 2 or row_sumsq.shape[0] != M \
+            or not row_sumsq.is_contiguous():
+        raise ValueError("linear_rowscale: row_sumsq must be a contiguous fp32 [M, P] tensor")
+    if epilogue is None:
+        epilogue = _lib.NSW_EPI_NONE if bias is None else (
+            _lib.NSW_EPI_BIAS if residual is None else _lib.NSW_EPI_BIAS_RESIDUAL)
+    eps = default_eps(x.dtype) if eps is None else float(eps)
+    y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=dev)
+    check(lib().nsw_linear_rowscale(x.data_ptr(), w_n.data_ptr(), _p(bias), _p(residual), y.data_ptr(),
+                                    row_sumsq.data_ptr(), row_sumsq.shape[1], M, N, K, int(epilogue), eps,
+                                    dtype_code(x), _stream(dev)), "linear_rowscale")
+    return y
+
+
 # ------------------------------------------------------------------- block ---
 
 _ws_lock = threading.Lock()

@@ -148,12 +148,15 @@ class Block(nn.Module):
         self._mask_cache = {}
         self._pack_key = None
         self._pack = None
-        # True runs norm1 / norm2 inside the GEMMs that consume them (5
-        # launches per block, row sums of squares from the GEMM's own
-        # fragments).  Off by default: on MI355X the extra VALU work in the
-        # GEMM main loop and the gathered QKV rows cost more than the two
-        # row passes they replace (block 2.14 vs 2.01 ms at 180x360, C=1024).
-        self.fuse_norms = False
+        # fold_norm2: the proj GEMM writes the row sums of squares of h1 and
+        # fc1 applies RMSNorm as a row scale with norm2's weight folded into
+        # W1 (no separate norm2 pass; 6 launches).  fold_norm1: also fold
+        # norm1 into the QKV GEMM, which then gathers the token rows and sums
+        # their squares in its main loop (5 launches) -- slower on MI355X than
+        # the separate norm1 gather (2.14 vs 2.01 ms at 180x360, C=1024), so
+        # off by default.
+        self.fold_norm1 = False
+        self.fold_norm2 = True
 
     # The reference registers attn_mask [nW, T*wa, T*wa] as a non-persistent
     # buffer (models/swin_helpers.py:397).  Here it is materialised on demand
@@ -200,13 +203,15 @@ class Block(nn.Module):
                 "b1": d(self.mlp.bias1.bias), "w2": d(self.mlp.fc2.weight), "b2": d(self.mlp.bias2.bias),
             }
             self._pack_key = key
-        if self.fuse_norms and "wqkv_n1" not in self._pack:
+        pk = self._pack
+        with torch.no_grad():
             # norm weights folded into the GEMM weights that consume the
             # normalised rows: RMSNorm(x) . W^T = rs(x) * (x . (W * norm_w)^T)
-            with torch.no_grad():
-                pk = self._pack
-                n1, n2 = pk["norm1_w"].float(), pk["norm2_w"].float()
+            if self.fold_norm1 and "wqkv_n1" not in pk:
+                n1 = pk["norm1_w"].float()
                 pk["wqkv_n1"] = (pk["wqkv"].float() * n1[None, :]).to(pk["wqkv"].dtype).contiguous()
+            if self.fold_norm2 and "w1_n2" not in pk:
+                n2 = pk["norm2_w"].float()
                 pk["w1_n2"] = (pk["w1"].float() * n2[None, :]).to(pk["w1"].dtype).contiguous()
         return self._pack
 
@@ -227,8 +232,9 @@ class Block(nn.Module):
             raise ValueError("temporal dim does not match temporal_context_window_size")
         self.mlp._check_fusable()
         pk = self.packed()
-        if not self.fuse_norms:
-            pk = {k: v for k, v in pk.items() if k not in ("wqkv_n1", "w1_n2")}
+        drop = ([] if self.fold_norm1 else ["wqkv_n1"]) + ([] if self.fold_norm2 else ["w1_n2"])
+        if drop:
+            pk = {k: v for k, v in pk.items() if k not in drop}
         return ops.swin_block_forward(x.contiguous(), pk, self.num_heads, self.window_size,
                                       self.shift_size, eps=self._eps(x.dtype))
 
