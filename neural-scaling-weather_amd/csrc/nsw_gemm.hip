@@ -4,11 +4,14 @@
 // Workgroup tile 256 (m) x TN (n), 4 wavefronts in a 2 x 2 grid, each owning
 // a 128 x TN/2 sub-tile of 16x16 fp32 accumulator blocks.  Two
 // configurations (Cfg<TN>):
-//   TN = 256: one workgroup per CU, LDS stages of 128 bytes of k per row
-//             (64 bf16) for the 256 x-rows and 256 w-rows (64 KB), 2 stages;
+//   TN = 256: one workgroup per CU; stages of 128 bytes of k per row (64
+//             bf16) for the 256 x-rows and the 256 w-rows; x in a ring of 3
+//             slots and w in a ring of 2 slots of 32 KB (all 160 KB of LDS),
+//             copies issued at a steady 8 per wave and MFMA step
+//             (mainloop_256);
 //   TN = 128: two workgroups per CU, stages of 64 bytes of k per row (24 KB),
 //             3 stages, so that one tile's epilogue overlaps the other's
-//             MFMAs (short K with a GELU, head-norm or scatter epilogue).
+//             MFMAs (short K with the GELU epilogue).
 // A stage of 128-byte rows is consumed as two MFMA steps of 32 bf16; its
 // copies read whole 128-byte lines, half as many line requests per byte as
 // 64-byte rows.
@@ -22,10 +25,11 @@
 //   64-byte rows:  g(r) = ((r >> 1) ^ (r >> 3)) & 3,
 //   128-byte rows: g(r) = ((r >> 1) & 7) ^ ((r & 1) << 2).
 //
-// Pipeline per MFMA step k (32 bf16 of k): when step k+1 starts a new stage,
-// wait for this wave's copies of that stage and its own fragment reads, then
-// barrier; the stage of step k is then free and the copies of stage
-// k/SUB + NSTAGE are issued into it, spread over the step's MFMA groups.  The
+// Pipeline of the 256 x 128 tile per MFMA step k (32 bf16 of k): when step
+// k+1 starts a new stage, wait for this wave's copies of that stage and its
+// own fragment reads, then barrier; the stage of step k is then free and the
+// copies of stage k/SUB + NSTAGE are issued into it, spread over the step's
+// MFMA groups (the 256 x 256 schedule is described at mainloop_256).  The
 // MFMAs of step k run from registers while the fragment reads of step k+1 are
 // interleaved between them (register double buffering).  The barrier is a
 // bare s_barrier: __syncthreads() would add a fence that waits for every
@@ -107,6 +111,9 @@ template <int TN> struct Cfg {
   static constexpr int WG_PER_CU = TN == 256 ? 1 : 2;
   static constexpr int UNROLL = (SUB * NSTAGE) % 2 == 0 ? SUB * NSTAGE : 2 * SUB * NSTAGE;
   static constexpr int STAGE_BYTES = (BM + BN) * ROWB;
+  // LDS of the operand ring: TN = 256 keeps x in 3 slots and w in 2 slots of
+  // 256 rows x 128 B (160 KB); TN = 128 a ring of NSTAGE whole stages
+  static constexpr int RING = TN == 256 ? 5 * 256 * 128 : NSTAGE * STAGE_BYTES;
   static constexpr int COPIES = STAGE_BYTES / (256 * 16);  // 16-byte copies per thread per stage
   static constexpr int CPG = (COPIES + MB - 1) / MB;       // copies per 8-MFMA group
 };
@@ -117,7 +124,7 @@ template <int TN> struct Cfg {
 // spread over the banks
 template <typename T, int TN> struct Stg {
   static constexpr int BUDGET = 160 * 1024 / Cfg<TN>::WG_PER_CU;
-  static constexpr int RING = Cfg<TN>::NSTAGE * Cfg<TN>::STAGE_BYTES;
+  static constexpr int RING = Cfg<TN>::RING;
   static constexpr int STRIDE = TN * (int)sizeof(T) + 16;
   static constexpr int ROWS = BM * STRIDE <= BUDGET ? BM : BM / 2;
   static constexpr int PASSES = BM / ROWS;
@@ -276,6 +283,133 @@ __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk)
   return *reinterpret_cast<const u32x4*>(stage + row * ROWB + slot * 16);
 }
 
+// Main loop of the 256 x 256 tile.  Stage st holds 128 bytes of k of the 256
+// x rows and the 256 w rows.  x lives in a ring of 3 slots and w in a ring of
+// 2 slots of 32 KB (160 KB in all), so that the copies of a stage are issued
+// at a steady 8 instructions per wave and MFMA step:
+//   step 2s+1 (the second step of stage s, after the barrier that frees the
+//              slots of stage s): w of stage s+2 into w slot s%2;
+//   step 2s+2 (the first step of stage s+1): x of stage s+3 into x slot s%3,
+// and the x copies (the operand with fewer sharers in L2) get 2-3 steps of
+// lead, the w copies 1-2.  At the start of step 2s+1 a wave waits for the
+// copies of stage s+1 (only x of stage s+2 may still be in flight), then
+// barrier.  Fragments of step k+1 are read during step k (register double
+// buffering), so a slot is free once the barrier at the start of the last
+// step of its stage has passed.
+template <typename T, int PRE>
+__device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X, const T* __restrict__ Wt, int M,
+                                             int N, int K, int m0, int n0, const EpiArgs& ea,
+                                             f32x4 (&acc)[8][8], float (&ssr)[8], int wave, int lane) {
+  constexpr int ROWB = 128;               // k bytes per row and stage
+  constexpr int SLOT = 256 * ROWB;        // one operand's stage: 32 KB
+  constexpr int NC = SLOT / (4 * 1024);   // copies per wave per operand and stage (8)
+  constexpr int UNR = 12;                 // steps per loop iteration: 6 stages, a multiple of 3 and 2
+  const uint32_t rowbytes = (uint32_t)K * sizeof(T);
+  const u32x4 rx = make_rsrc(X, (uint32_t)M * rowbytes);
+  const u32x4 rw = make_rsrc(Wt, (uint32_t)N * rowbytes);
+  // copy j of this wave covers slot rows wave*64 + 8j .. +7; lane i writes row
+  // +i/8, 16-byte slot i%8, and loads global chunk slot ^ swizzle(row)
+  uint32_t vx[NC], vw[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int srow = wave * 64 + j * 8 + lane / 8;
+    const int chunk = (lane % 8) ^ row_swizzle<ROWB>(srow);
+    int gx = m0 + srow;
+    gx = gx < M ? gx : M - 1;   // rows past the edge re-read the last row (never stored)
+    if constexpr (PRE == PRE_ROWNORM_GATHER) gx = (int)ea.geom.token_of_row(gx);
+    int gw = n0 + srow;
+    gw = gw < N ? gw : N - 1;
+    vx[j] = (uint32_t)gx * rowbytes + chunk * 16;
+    vw[j] = (uint32_t)gw * rowbytes + chunk * 16;
+  }
+  const uint32_t cbase = (uint32_t)(uintptr_t)smem + wave * 64 * ROWB;   // this wave's first slot row
+
+#define NSW_XSLOT(s) (((s) % 3) * SLOT)
+#define NSW_WSLOT(s) ((3 + (s) % 2) * SLOT)
+// copy j of stage st (k bytes st*ROWB ..) into the slot of stage sl (sl == st
+// modulo 6; sl is a compile-time constant)
+#define NSW_COPY_X(sl, st, j) dma16(rx, cbase + NSW_XSLOT(sl) + (j) * 1024, vx[j], (st) * ROWB)
+#define NSW_COPY_W(sl, st, j) dma16(rw, cbase + NSW_WSLOT(sl) + (j) * 1024, vw[j], (st) * ROWB)
+
+  const int nk = K / (STEPB / (int)sizeof(T));   // MFMA steps
+  const int nst = nk / 2;                          // stages
+  // prologue: x0 w0 x1 w1 x2, then wait for x0 and w0
+#pragma unroll
+  for (int j = 0; j < NC; ++j) NSW_COPY_X(0, 0, j);
+#pragma unroll
+  for (int j = 0; j < NC; ++j) NSW_COPY_W(0, 0, j);
+  if (nst > 1) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) NSW_COPY_X(1, 1, j);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) NSW_COPY_W(1, 1, j);
+  }
+  if (nst > 2) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) NSW_COPY_X(2, 2, j);
+    NSW_WAIT_VMCNT(3 * NC);
+  } else if (nst > 1) {
+    NSW_WAIT_VMCNT(2 * NC);
+  } else {
+    NSW_WAIT_VMCNT(0);
+  }
+  wg_barrier();
+
+  const int frow = lane & 15, fg = lane >> 4;
+  const int wrow = (wave & 1) * 128 + frow;    // w rows of this wave (A operand)
+  const int xrow = (wave >> 1) * 128 + frow;   // x rows of this wave (B operand)
+  u32x4 fa[2][8], fb[2][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) fa[0][i] = lds_frag<ROWB>(smem + NSW_WSLOT(0), wrow + i * 16, fg);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) fb[0][i] = lds_frag<ROWB>(smem + NSW_XSLOT(0), xrow + i * 16, fg);
+
+  // step k = kt + U of stage st = k/2; kt is a multiple of UNR, so the slots
+  // of the stages touched by step U are compile-time constants
+#define NSW_STEP256(U)                                                                         \
+  {                                                                                            \
+    const int k = kt + U;                                                                      \
+    if (k < nk) {                                                                              \
+      constexpr int sub_ = (U) % 2, su_ = (U) / 2;                                             \
+      constexpr int nsub_ = ((U) + 1) % 2, nsu_ = ((U) + 1) / 2;                               \
+      const int st = k >> 1;                                                                   \
+      if (sub_ == 1 && k + 1 < nk) {                                                           \
+        if (st + 2 < nst) NSW_WAIT_VMCNT(NC);                                                  \
+        else NSW_WAIT_VMCNT(0);                                                                \
+        NSW_WAIT_LGKMCNT0();                                                                   \
+        wg_barrier();                                                                          \
+      }                                                                                        \
+      const bool cp_ = sub_ == 1 ? st + 2 < nst : (k >= 2 && st + 2 < nst);                    \
+      _Pragma("unroll") for (int mb = 0; mb < 8; ++mb) {                                       \
+        if (cp_) {                                                                             \
+          if (sub_ == 1) NSW_COPY_W(su_ + 2, st + 2, mb);                                      \
+          else NSW_COPY_X(su_ + 2, st + 2, mb);                                                \
+        }                                                                                      \
+        /* unconditional: after the last step these read stale slots (unused); a  */         \
+        /* conditional read would make the wait-count pass drain all LDS reads   */         \
+        fb[((U) + 1) & 1][mb] = lds_frag<ROWB>(smem + NSW_XSLOT(nsu_), xrow + mb * 16, nsub_ * 4 + fg); \
+        fa[((U) + 1) & 1][mb] = lds_frag<ROWB>(smem + NSW_WSLOT(nsu_), wrow + mb * 16, nsub_ * 4 + fg); \
+        _Pragma("unroll") for (int nb = 0; nb < 8; ++nb)                                       \
+          mfma_chunk<T>(acc[nb][mb], fa[(U) & 1][nb], fb[(U) & 1][mb]);                        \
+        if constexpr (pre_sums_in_loop(PRE)) ssr[mb] = frag_sumsq<T>(fb[(U) & 1][mb], ssr[mb]); \
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                                     \
+        __builtin_amdgcn_sched_group_barrier(0x008, 8 * (sizeof(T) == 2 ? 1 : 4), 0);          \
+      }                                                                                        \
+    }                                                                                          \
+  }
+
+  for (int kt = 0; kt < nk; kt += UNR) {
+    NSW_STEP256(0) NSW_STEP256(1) NSW_STEP256(2) NSW_STEP256(3)
+    NSW_STEP256(4) NSW_STEP256(5) NSW_STEP256(6) NSW_STEP256(7)
+    NSW_STEP256(8) NSW_STEP256(9) NSW_STEP256(10) NSW_STEP256(11)
+  }
+#undef NSW_STEP256
+#undef NSW_COPY_X
+#undef NSW_COPY_W
+#undef NSW_XSLOT
+#undef NSW_WSLOT
+}
+
 template <typename T, int EPI, int TN, int PRE>
 __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* __restrict__ X,
                                                                       const T* __restrict__ Wt,
@@ -310,6 +444,19 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   const int mt = gm0 + tin % gsz, nt = tin / gsz;
   const int m0 = mt * BM, n0 = nt * BN;
 
+  f32x4 acc[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ssr[MB];                                  // PRE: this lane's part of the row sums of squares
+#pragma unroll
+  for (int i = 0; i < MB; ++i) ssr[i] = 0.f;
+  const int frow = lane & 15, fg = lane >> 4;
+
+  if constexpr (TN == 256) {
+    mainloop_256<T, PRE>(smem, X, Wt, M, N, K, m0, n0, ea, acc, ssr, wave, lane);
+  } else {
   // ---- copy plan: the stage holds the BM x rows, then the BN w rows
   const uint32_t rowbytes = (uint32_t)K * sizeof(T);
   CopyPlan<COPIES> cp;
@@ -333,21 +480,11 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
     }
   }
 
-  f32x4 acc[NB][MB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i)
-#pragma unroll
-    for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int frow = lane & 15, fg = lane >> 4;
   const int arow = BM + wn * WTN + frow;   // w rows of this wave (A operand)
   const int brow = wm * WTM + frow;        // x rows of this wave (B operand)
   const int nk = K / (STEPB / (int)sizeof(T));   // MFMA steps
   const int nst = nk / SUB;                       // LDS stages
   u32x4 fa[2][NB], fb[2][MB];
-  float ssr[MB];                                  // PRE: this lane's part of the row sums of squares
-#pragma unroll
-  for (int i = 0; i < MB; ++i) ssr[i] = 0.f;
 
 #define NSW_STAGE(i) (smem + ((i) % NSTAGE) * STAGE_BYTES)
 #define NSW_WAIT_AHEAD(ahead)                                                                  \
@@ -419,6 +556,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
 #undef NSW_WAIT_AHEAD
 #undef NSW_STAGE
   static_assert(UNROLL % 2 == 0 && UNROLL <= 8, "unroll");
+  }
 
   // ---------------------------------------------------------------- epilogue
   // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
@@ -586,46 +724,63 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
       }
     }
     wg_barrier();
+    // rows are copied out in batches: all staging reads of a batch are issued
+    // before its stores, so that one LDS round trip covers BATCH rows (the
+    // reads are always in bounds; only the stores are predicated)
+    constexpr int BATCH = ITER < 8 ? ITER : 8;
+    static_assert(ITER % BATCH == 0, "batch");
 #pragma unroll
-    for (int it = 0; it < ITER; ++it) {
-      const int rl = (wave * ITER + it) * RPI + lrow;
-      const int m = m0 + prow0 + rl;
-      float ssq = 0.f;                                // sum of squares of this lane's stored values
-      if (m < M && n < N) {
-        int64_t orow = m;
-        if constexpr (SCAT) orow = otok[it];
-        float o[VEC];
-        load16<T>(reinterpret_cast<const T*>(stg + rl * S::STRIDE) + col, o);
-        if constexpr (RES) {
-          float rv[VEC];
-          if constexpr (sizeof(T) == 2) {
-            const bf16x8 rb = __builtin_bit_cast(bf16x8, rres[it]);
+    for (int ib = 0; ib < ITER; ib += BATCH) {
+      u32x4 ov[BATCH];
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) rv[e] = (float)rb[e];
-          } else {
-            const f32x4 rf = __builtin_bit_cast(f32x4, rres[it]);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) rv[e] = rf[e];
-          }
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) o[e] += rv[e];
-        }
-        store16<T>(Y + orow * N + n, o);
-        if constexpr (SCAT) {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            const float r = sizeof(T) == 2 ? (float)(T)o[e] : o[e];   // the stored value
-            ssq = fmaf(r, r, ssq);
-          }
-        }
+      for (int b = 0; b < BATCH; ++b) {
+        const int rl = (wave * ITER + ib + b) * RPI + lrow;
+        ov[b] = *reinterpret_cast<const u32x4*>(stg + rl * S::STRIDE + col * (int)sizeof(T));
       }
-      if constexpr (SCAT) {
-        // partial sum of squares over the 16 lanes (16 * VEC columns) of a
-        // DPP row, one float per 256 bytes of output row
-        if (ea.row_sumsq != nullptr) {
-          ssq = row16_sum(ssq);
-          if ((lane & 15) == 0 && m < M && n < N)
-            ea.row_sumsq[(int64_t)otok[it] * ea.nparts + n / (16 * VEC)] = ssq;
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+        const int it = ib + b;
+        const int rl = (wave * ITER + it) * RPI + lrow;
+        const int m = m0 + prow0 + rl;
+        float ssq = 0.f;                              // sum of squares of this lane's stored values
+        if (m < M && n < N) {
+          int64_t orow = m;
+          if constexpr (SCAT) orow = otok[it];
+          if constexpr (RES) {
+            float o[VEC], rv[VEC];
+            if constexpr (sizeof(T) == 2) {
+              const bf16x8 ob = __builtin_bit_cast(bf16x8, ov[b]);
+              const bf16x8 rb = __builtin_bit_cast(bf16x8, rres[it]);
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) { o[e] = (float)ob[e]; rv[e] = (float)rb[e]; }
+            } else {
+              const f32x4 of = __builtin_bit_cast(f32x4, ov[b]);
+              const f32x4 rf = __builtin_bit_cast(f32x4, rres[it]);
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) { o[e] = of[e]; rv[e] = rf[e]; }
+            }
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) o[e] += rv[e];
+            store16<T>(Y + orow * N + n, o);
+            if constexpr (SCAT) {
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) {
+                const float r = sizeof(T) == 2 ? (float)(T)o[e] : o[e];   // the stored value
+                ssq = fmaf(r, r, ssq);
+              }
+            }
+          } else {
+            *reinterpret_cast<u32x4*>(Y + orow * N + n) = ov[b];
+          }
+        }
+        if constexpr (SCAT) {
+          // partial sum of squares over the 16 lanes (16 * VEC columns) of a
+          // DPP row, one float per 256 bytes of output row
+          if (ea.row_sumsq != nullptr) {
+            ssq = row16_sum(ssq);
+            if ((lane & 15) == 0 && m < M && n < N)
+              ea.row_sumsq[(int64_t)otok[it] * ea.nparts + n / (16 * VEC)] = ssq;
+          }
         }
       }
     }
@@ -655,11 +810,11 @@ static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t
                     ((uintptr_t)ea.residual % 16) == 0,
                 "%s: x, w, y and residual must be 16-byte aligned", what);
   NSW_CHECK_ARG(((M + BM - 1) / BM) * ((N + 127) / 128) < (1LL << 31), "%s: too many tiles", what);
-  // Short K with a heavy epilogue (GELU, head norm, row scatter): 256x128,
-  // two workgroups per CU overlap one tile's epilogue with the other's MFMAs.
-  // Otherwise the 256x256 main loop.
-  constexpr bool heavy = EPI == EPI_BIAS_GELU || EPI == EPI_SCATTER_RESIDUAL || qkv_head_dim(EPI) > 0;
-  if (heavy && K <= 2048) launch_tiles<T, EPI, 128, PRE>(x, w, y, M, N, K, ea, st);
+  // Short K with the GELU epilogue (~23 VALU slots per output): 256x128, two
+  // workgroups per CU overlap one tile's epilogue with the other's MFMAs.
+  // Otherwise (head norm and row scatter included, measured faster there)
+  // the 256x256 main loop.
+  if (EPI == EPI_BIAS_GELU && K <= 2048) launch_tiles<T, EPI, 128, PRE>(x, w, y, M, N, K, ea, st);
   else launch_tiles<T, EPI, 256, PRE>(x, w, y, M, N, K, ea, st);
   return check_launch(what);
 }
