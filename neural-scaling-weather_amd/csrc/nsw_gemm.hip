@@ -423,8 +423,8 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   constexpr int UNROLL = Cfg<TN>::UNROLL;
   constexpr int STAGE_BYTES = Cfg<TN>::STAGE_BYTES;
   constexpr int COPIES = Cfg<TN>::COPIES;
-  // the 4-stage operand ring during the k loop, the output staging area in
-  // the epilogue
+  // the operand ring during the k loop, the output staging area in the
+  // epilogue
   __shared__ __attribute__((aligned(1024))) char smem[Stg<T, TN>::SMEM];
 
   const int tid = threadIdx.x;
@@ -519,7 +519,9 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
         NSW_WAIT_LGKMCNT0();                                                                   \
         wg_barrier();                                                                          \
       }                                                                                        \
-      const char* nx = (k + 1 < nk) ? NSW_STAGE(sn_) : cur;                                    \
+      /* the next step's stage, also after the last step (a stale, unused read */         \
+      /* that keeps the fragment addresses compile-time offsets)               */         \
+      const char* nx = NSW_STAGE(sn_);                                                         \
       const int snext = k / SUB + NSTAGE;                                                      \
       _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                      \
         if (bnd_ && snext < nst) {                                                             \
@@ -631,10 +633,9 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
     for (int mb = 0; mb < MB; ++mb) rsr[mb] = 1.0f / sqrtf(ss[mb] / (float)K + ea.eps);
   }
 
-  // 1. epilogue math in the fragment layout, in place
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    float v[NB][4];
+  // 1. epilogue math of row block mb in the fragment layout (bias, row scale,
+  // head norm, GELU), evaluated where the block is staged
+  auto row_values = [&](int mb, float (&v)[NB][4]) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -646,17 +647,18 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
       float ss[NHW];
 #pragma unroll
       for (int h = 0; h < NHW; ++h) {
-        float s = 0.f;
+        float sh = 0.f;
 #pragma unroll
         for (int b = 0; b < NBH; ++b)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) s += v[h * NBH + b][r] * v[h * NBH + b][r];
-        ss[h] = rows4_sum(s);
+          for (int r = 0; r < 4; ++r) sh = fmaf(v[h * NBH + b][r], v[h * NBH + b][r], sh);
+        ss[h] = rows4_sum(sh);
       }
 #pragma unroll
       for (int h = 0; h < NHW; ++h) {
         if (normed[h]) {
-          const float rs = 1.0f / sqrtf(ss[h] / (float)HDQ + ea.eps);
+          // x * rsqrt(mean(x^2) + eps), then * weight, as RMSNorm
+          const float rs = __builtin_amdgcn_rsqf(ss[h] * (1.0f / (float)HDQ) + ea.eps);
 #pragma unroll
           for (int b = 0; b < NBH; ++b)
 #pragma unroll
@@ -670,116 +672,113 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[nb][r] = gelu_erf(v[nb][r]);
     }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb][mb] = f32x4{v[nb][0], v[nb][1], v[nb][2], v[nb][3]};
-  }
+  };
 
   // 2. write-out through LDS: the waves owning the staged rows store their
-  // values in the fragment layout (output dtype), then every wave copies
-  // whole rows out with 16-byte lane accesses (fully coalesced), adding the
-  // residual there.  The residual rows are loaded before the barrier so that
-  // their latency overlaps the staging.
+  // values in the fragment layout (output dtype), which frees the
+  // accumulators, then every wave copies whole rows out with 16-byte lane
+  // accesses (fully coalesced) in batches of BATCH rows, adding the residual
+  // there.  A batch's output rows (the window -> token map for the scatter)
+  // and residual rows are loaded one batch ahead, the first batch's before
+  // the staging writes; the loads use clamped addresses (no branches), only
+  // the stores are predicated.
   using S = Stg<T, TN>;
   constexpr int VEC = 16 / sizeof(T);                 // elements per 16-byte chunk
   constexpr int LPR = BN / VEC;                       // lanes per output row (32 bf16 / 64 f32)
   constexpr int RPI = 64 / LPR;                       // rows per copy instruction (2 / 1)
   constexpr int ITER = S::ROWS / 4 / RPI;             // copy instructions per wave per pass
+  constexpr int BATCH = ITER < 8 ? ITER : 8;
+  constexpr int NBAT = ITER / BATCH;
+  static_assert(ITER % BATCH == 0, "batch");
   constexpr bool RES = EPI == EPI_BIAS_RESIDUAL || EPI == EPI_SCATTER_RESIDUAL;
+  constexpr bool SCAT = EPI == EPI_SCATTER_RESIDUAL;
   NSW_WAIT_LGKMCNT0();
   wg_barrier();                                       // the operand ring is no longer read
   char* stg = smem;
   const int lrow = lane / LPR;                        // row of this lane within an instruction
   const int col = (lane % LPR) * VEC;                 // first tile column of this lane
   const int n = n0 + col;
+  const int nc = n < N ? n : 0;                       // clamped column for loads
 #pragma unroll
   for (int pass = 0; pass < S::PASSES; ++pass) {
     const int prow0 = pass * S::ROWS;                 // first tile row of this pass
-    // residual prefetch for this wave's rows of the pass
-    u32x4 rres[RES ? ITER : 1];
-    constexpr bool SCAT = EPI == EPI_SCATTER_RESIDUAL;
-    int otok[SCAT ? ITER : 1];                        // output token of each row (scatter), mapped once
-    if constexpr (RES) {
+    int orow[2][BATCH];                               // output row (token for the scatter) per batch row
+    u32x4 rres[2][RES ? BATCH : 1];
+    auto prefetch = [&](int ib, int slot) {
 #pragma unroll
-      for (int it = 0; it < ITER; ++it) {
-        const int rl = (wave * ITER + it) * RPI + lrow;
-        const int m = m0 + prow0 + rl;
-        rres[it] = u32x4{0u, 0u, 0u, 0u};
-        if constexpr (SCAT) otok[it] = m < M ? (int)ea.geom.token_of_row(m) : 0;
-        if (m < M && n < N) {
-          int64_t orow = m;
-          if constexpr (SCAT) orow = otok[it];
-          rres[it] = *reinterpret_cast<const u32x4*>((const T*)ea.residual + orow * N + n);
-        }
+      for (int b = 0; b < BATCH; ++b) {
+        const int rl = (wave * ITER + ib * BATCH + b) * RPI + lrow;
+        int m = m0 + prow0 + rl;
+        m = m < M ? m : M - 1;
+        if constexpr (SCAT) orow[slot][b] = (int)ea.geom.token_of_row(m);
+        else orow[slot][b] = m;
+        if constexpr (RES)
+          rres[slot][b] = *reinterpret_cast<const u32x4*>((const T*)ea.residual + (int64_t)orow[slot][b] * N + nc);
       }
-    }
+    };
+    prefetch(0, 0);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const int trow = wm * WTM + mb * 16 + frow - prow0;
-      if (trow >= 0 && trow < S::ROWS) {
+      if (wm * WTM + mb * 16 - prow0 >= 0 && wm * WTM + mb * 16 - prow0 < S::ROWS) {   // wave-uniform
+        float v[NB][4];
+        row_values(mb, v);
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          float v4[4] = {acc[nb][mb][0], acc[nb][mb][1], acc[nb][mb][2], acc[nb][mb][3]};
-          store4<T>(reinterpret_cast<T*>(stg + trow * S::STRIDE) + wn * WTN + nb * 16 + fg * 4, v4);
-        }
+        for (int nb = 0; nb < NB; ++nb) store4<T>(reinterpret_cast<T*>(stg + trow * S::STRIDE) + wn * WTN + nb * 16 + fg * 4, v[nb]);
       }
     }
     wg_barrier();
-    // rows are copied out in batches: all staging reads of a batch are issued
-    // before its stores, so that one LDS round trip covers BATCH rows (the
-    // reads are always in bounds; only the stores are predicated)
-    constexpr int BATCH = ITER < 8 ? ITER : 8;
-    static_assert(ITER % BATCH == 0, "batch");
 #pragma unroll
-    for (int ib = 0; ib < ITER; ib += BATCH) {
+    for (int ib = 0; ib < NBAT; ++ib) {
+      const int cur = ib & 1;
+      if (ib + 1 < NBAT) prefetch(ib + 1, cur ^ 1);
       u32x4 ov[BATCH];
 #pragma unroll
       for (int b = 0; b < BATCH; ++b) {
-        const int rl = (wave * ITER + ib + b) * RPI + lrow;
+        const int rl = (wave * ITER + ib * BATCH + b) * RPI + lrow;
         ov[b] = *reinterpret_cast<const u32x4*>(stg + rl * S::STRIDE + col * (int)sizeof(T));
       }
 #pragma unroll
       for (int b = 0; b < BATCH; ++b) {
-        const int it = ib + b;
-        const int rl = (wave * ITER + it) * RPI + lrow;
+        const int rl = (wave * ITER + ib * BATCH + b) * RPI + lrow;
         const int m = m0 + prow0 + rl;
+        const bool ok = m < M && n < N;
         float ssq = 0.f;                              // sum of squares of this lane's stored values
-        if (m < M && n < N) {
-          int64_t orow = m;
-          if constexpr (SCAT) orow = otok[it];
-          if constexpr (RES) {
-            float o[VEC], rv[VEC];
-            if constexpr (sizeof(T) == 2) {
-              const bf16x8 ob = __builtin_bit_cast(bf16x8, ov[b]);
-              const bf16x8 rb = __builtin_bit_cast(bf16x8, rres[it]);
+        if constexpr (RES) {
+          float o[VEC], rv[VEC];
+          if constexpr (sizeof(T) == 2) {
+            const bf16x8 ob = __builtin_bit_cast(bf16x8, ov[b]);
+            const bf16x8 rb = __builtin_bit_cast(bf16x8, rres[cur][b]);
 #pragma unroll
-              for (int e = 0; e < VEC; ++e) { o[e] = (float)ob[e]; rv[e] = (float)rb[e]; }
-            } else {
-              const f32x4 of = __builtin_bit_cast(f32x4, ov[b]);
-              const f32x4 rf = __builtin_bit_cast(f32x4, rres[it]);
-#pragma unroll
-              for (int e = 0; e < VEC; ++e) { o[e] = of[e]; rv[e] = rf[e]; }
-            }
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) o[e] += rv[e];
-            store16<T>(Y + orow * N + n, o);
-            if constexpr (SCAT) {
-#pragma unroll
-              for (int e = 0; e < VEC; ++e) {
-                const float r = sizeof(T) == 2 ? (float)(T)o[e] : o[e];   // the stored value
-                ssq = fmaf(r, r, ssq);
-              }
-            }
+            for (int e = 0; e < VEC; ++e) { o[e] = (float)ob[e]; rv[e] = (float)rb[e]; }
           } else {
-            *reinterpret_cast<u32x4*>(Y + orow * N + n) = ov[b];
+            const f32x4 of = __builtin_bit_cast(f32x4, ov[b]);
+            const f32x4 rf = __builtin_bit_cast(f32x4, rres[cur][b]);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) { o[e] = of[e]; rv[e] = rf[e]; }
           }
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[e] += rv[e];
+          if (ok) store16<T>(Y + (int64_t)orow[cur][b] * N + n, o);
+          if constexpr (SCAT) {
+            // only stored elements count (lanes past N or rows past M add 0)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+              const float r = sizeof(T) == 2 ? (float)(T)o[e] : o[e];   // the stored value
+              ssq = fmaf(r, r, ssq);
+            }
+            if (!ok) ssq = 0.f;
+          }
+        } else {
+          if (ok) *reinterpret_cast<u32x4*>(Y + (int64_t)orow[cur][b] * N + n) = ov[b];
         }
         if constexpr (SCAT) {
           // partial sum of squares over the 16 lanes (16 * VEC columns) of a
           // DPP row, one float per 256 bytes of output row
           if (ea.row_sumsq != nullptr) {
             ssq = row16_sum(ssq);
-            if ((lane & 15) == 0 && m < M && n < N)
-              ea.row_sumsq[(int64_t)otok[it] * ea.nparts + n / (16 * VEC)] = ssq;
+            if ((lane & 15) == 0 && ok)
+              ea.row_sumsq[(int64_t)orow[cur][b] * ea.nparts + n / (16 * VEC)] = ssq;
           }
         }
       }
@@ -814,8 +813,12 @@ static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t
   // workgroups per CU overlap one tile's epilogue with the other's MFMAs.
   // Otherwise (head norm and row scatter included, measured faster there)
   // the 256x256 main loop.
-  if (EPI == EPI_BIAS_GELU && K <= 2048) launch_tiles<T, EPI, 128, PRE>(x, w, y, M, N, K, ea, st);
-  else launch_tiles<T, EPI, 256, PRE>(x, w, y, M, N, K, ea, st);
+  if constexpr (EPI == EPI_BIAS_GELU) {
+    if (K <= 2048) launch_tiles<T, EPI, 128, PRE>(x, w, y, M, N, K, ea, st);
+    else launch_tiles<T, EPI, 256, PRE>(x, w, y, M, N, K, ea, st);
+  } else {
+    launch_tiles<T, EPI, 256, PRE>(x, w, y, M, N, K, ea, st);
+  }
   return check_launch(what);
 }
 
