@@ -1,38 +1,23 @@
 // MFMA GEMM y[M,N] = epilogue(x[M,K] . w[N,K]^T) for gfx950, with the Swin
 // block's epilogues fused in.
 //
-// Workgroup tile 256 (m) x TN (n), 4 wavefronts in a 2 x 2 grid, each owning
-// a 128 x TN/2 sub-tile of 16x16 fp32 accumulator blocks.  Two
-// configurations (Cfg<TN>):
-//   TN = 256: one workgroup per CU; stages of 128 bytes of k per row (64
-//             bf16) for the 256 x-rows and the 256 w-rows; x in a ring of 3
-//             slots and w in a ring of 2 slots of 32 KB (all 160 KB of LDS),
-//             copies issued at a steady 8 per wave and MFMA step
-//             (mainloop_256);
-//   TN = 128: two workgroups per CU, stages of 64 bytes of k per row (24 KB),
-//             3 stages, so that one tile's epilogue overlaps the other's
-//             MFMAs (short K with the GELU epilogue).
-// A stage of 128-byte rows is consumed as two MFMA steps of 32 bf16; its
-// copies read whole 128-byte lines, half as many line requests per byte as
-// 64-byte rows.
+// Workgroup tile 256 (m) x 256 (n), one workgroup of 4 wavefronts per CU in a
+// 2 x 2 grid, each owning a 128 x 128 sub-tile of 16x16 fp32 accumulator
+// blocks (256 accumulator registers per lane).  A stage holds 128 bytes of k
+// (64 bf16) of the 256 x-rows and the 256 w-rows and is consumed as two MFMA
+// steps of 32 bf16; x lives in a ring of 3 slots and w in a ring of 2 slots of
+// 32 KB (all 160 KB of LDS), filled at a steady 8 copies per wave and MFMA
+// step (schedule at mainloop_256).  Whole 128-byte lines per copy.
 //
 // Operand staging: global -> LDS copies use gfx950's buffer_load_dwordx4 ...
-// lds (direct to LDS, no VGPR staging): each instruction writes 1 KB = 1024 /
-// ROWB stage rows of one wave's share.  Rows are XOR-swizzled in 16-byte
-// chunks so that a fragment read (16 rows, same chunk) is bank-conflict free
-// whether ds_read_b128 is served in 8-lane phases over 32 banks or 16-lane
-// phases over 64 banks: slot = chunk ^ g(row & 15) with
-//   64-byte rows:  g(r) = ((r >> 1) ^ (r >> 3)) & 3,
-//   128-byte rows: g(r) = ((r >> 1) & 7) ^ ((r & 1) << 2).
-//
-// Pipeline of the 256 x 128 tile per MFMA step k (32 bf16 of k): when step
-// k+1 starts a new stage, wait for this wave's copies of that stage and its
-// own fragment reads, then barrier; the stage of step k is then free and the
-// copies of stage k/SUB + NSTAGE are issued into it, spread over the step's
-// MFMA groups (the 256 x 256 schedule is described at mainloop_256).  The
-// MFMAs of step k run from registers while the fragment reads of step k+1 are
-// interleaved between them (register double buffering).  The barrier is a
-// bare s_barrier: __syncthreads() would add a fence that waits for every
+// lds (direct to LDS, no VGPR staging): each instruction writes 1 KB = 8 stage
+// rows of one wave's share.  Rows are XOR-swizzled in 16-byte chunks so that a
+// fragment read (16 rows, same chunk) is bank-conflict free whether
+// ds_read_b128 is served in 8-lane phases over 32 banks or 16-lane phases over
+// 64 banks: slot = chunk ^ g(row & 15), g(r) = ((r >> 1) & 7) ^ ((r & 1) << 2).
+// The MFMAs of step k run from registers while the fragment reads of step k+1
+// are interleaved between them (register double buffering).  Barriers are bare
+// s_barrier: __syncthreads() would add a fence that waits for every
 // outstanding copy.
 //
 // The MFMA is issued "transposed": the A operand is the weight fragment
@@ -92,45 +77,24 @@ constexpr int WTM = 128;            // wave tile (m)
 constexpr int MB = WTM / 16;        // 16x16 result blocks per wave along m
 constexpr int STEPB = 64;           // k bytes per row consumed by one MFMA step
 
-// Two tile configurations (template parameter TN = weight rows per tile):
-//   TN = 256: 256 x 256 tile, 4 waves of 128 x 128, 2 stages of 128-byte
-//             rows (128 KB), one workgroup per CU;
-//   TN = 128: 256 x 128 tile, 4 waves of 128 x 64, 3 stages of 64-byte rows
-//             (72 KB), two workgroups per CU, so that one tile's prologue,
-//             barriers and epilogue overlap the other's MFMAs — measured
-//             best for short K (<= 2048) with a heavy epilogue (GELU, head
-//             norm, row scatter).
-template <int TN> struct Cfg {
-  static constexpr int BN = TN;                         // weight rows (n) per tile
-  static constexpr int WTN = TN / 2;                    // wave tile (n)
-  static constexpr int NB = WTN / 16;                   // 16x16 blocks per wave along n
-  static constexpr int ROWB = TN == 256 ? 128 : 64;     // k bytes per row per LDS stage
-  static constexpr int SUB = ROWB / STEPB;              // MFMA steps per stage
-  static constexpr int RPC = 1024 / ROWB;               // stage rows per copy instruction
-  static constexpr int NSTAGE = TN == 256 ? 2 : 3;      // LDS ring depth (128 KB / 72 KB)
-  static constexpr int WG_PER_CU = TN == 256 ? 1 : 2;
-  static constexpr int UNROLL = (SUB * NSTAGE) % 2 == 0 ? SUB * NSTAGE : 2 * SUB * NSTAGE;
-  static constexpr int STAGE_BYTES = (BM + BN) * ROWB;
-  // LDS of the operand ring: TN = 256 keeps x in 3 slots and w in 2 slots of
-  // 256 rows x 128 B (160 KB); TN = 128 a ring of NSTAGE whole stages
-  static constexpr int RING = TN == 256 ? 5 * 256 * 128 : NSTAGE * STAGE_BYTES;
-  static constexpr int COPIES = STAGE_BYTES / (256 * 16);  // 16-byte copies per thread per stage
-  static constexpr int CPG = (COPIES + MB - 1) / MB;       // copies per 8-MFMA group
-};
+constexpr int BN = 256;             // weight rows (n) per workgroup tile
+constexpr int WTN = 128;            // wave tile (n)
+constexpr int NB = WTN / 16;        // 16x16 result blocks per wave along n
+constexpr int ROWB = 128;           // k bytes per row and LDS stage (two MFMA steps)
+// LDS of the operand ring: x in 3 slots and w in 2 slots of 256 rows x 128 B
+constexpr int RING = 5 * 256 * ROWB;
+constexpr int LDS_BUDGET = 160 * 1024;
 
 // epilogue staging of the output tile in LDS, in the output dtype: the whole
-// 256-row tile when it fits in the workgroup's share of the CU's 160 KB,
-// else two halves; rows padded by 16 B so that the fragment-layout writes
-// spread over the banks
-template <typename T, int TN> struct Stg {
-  static constexpr int BUDGET = 160 * 1024 / Cfg<TN>::WG_PER_CU;
-  static constexpr int RING = Cfg<TN>::RING;
-  static constexpr int STRIDE = TN * (int)sizeof(T) + 16;
-  static constexpr int ROWS = BM * STRIDE <= BUDGET ? BM : BM / 2;
+// 256-row tile when it fits in the CU's 160 KB, else two halves; rows padded
+// by 16 B so that the fragment-layout writes spread over the banks
+template <typename T> struct Stg {
+  static constexpr int STRIDE = BN * (int)sizeof(T) + 16;
+  static constexpr int ROWS = BM * STRIDE <= LDS_BUDGET ? BM : BM / 2;
   static constexpr int PASSES = BM / ROWS;
   static constexpr int BYTES = ROWS * STRIDE;
   static constexpr int SMEM = RING > BYTES ? RING : BYTES;
-  static_assert(SMEM <= BUDGET, "LDS use exceeds the workgroup's share of the CU");
+  static_assert(SMEM <= LDS_BUDGET, "LDS use exceeds the CU's 160 KB");
 };
 
 struct EpiArgs {
@@ -146,21 +110,26 @@ struct EpiArgs {
 };
 
 // GELU with the exact-erf form of nn.GELU(): 0.5 v (1 + erf(v / sqrt 2)).
-// erf from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7):
-//   erf(x) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-x^2),
-//   t = 1 / (1 + p x), x >= 0, odd symmetry for x < 0.
-// 1 + erf(x) is formed without cancellation for x < 0 (it equals the tail q).
+// erfc from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7):
+//   erfc(x) = (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-x^2),
+//   t = 1 / (1 + p x), x >= 0.
+// With x = |v| / sqrt 2: 1 + erf(v / sqrt 2) is 2 - erfc(x) for v >= 0 and
+// erfc(x) for v < 0, so GELU(v) = max(v, 0) - |v| erfc(x) / 2 for both signs
+// (no select, no cancellation).  Constants folded: u = |v| sqrt(log2(e) / 2)
+// gives exp(-x^2) = exp2(-u^2) and p x = (p / (sqrt(log2(e)/2) sqrt 2)) u;
+// the polynomial coefficients carry the factor -1/2.  13 VALU instructions,
+// two of them transcendental (v_exp_f32, v_rcp_f32).
 __device__ __forceinline__ float gelu_erf(float v) {
-  const float x = fabsf(v) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, x, 1.0f));
-  float poly = fmaf(1.061405429f, t, -1.453152027f);
-  poly = fmaf(poly, t, 1.421413741f);
-  poly = fmaf(poly, t, -0.284496736f);
-  poly = fmaf(poly, t, 0.254829592f);
-  poly *= t;
-  const float q = poly * __expf(-x * x);     // 1 - erf(|x|)
-  const float one_plus_erf = v >= 0.f ? 2.0f - q : q;
-  return 0.5f * v * one_plus_erf;
+  const float a = fabsf(v);
+  const float u = a * 0.84932180028801907f;
+  const float e = __builtin_amdgcn_exp2f(-(u * u));
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.27273748087922252f, u, 1.0f));
+  float h = fmaf(-0.5307027145f, t, 0.7265760135f);
+  h = fmaf(h, t, -0.7107068705f);
+  h = fmaf(h, t, 0.142248368f);
+  h = fmaf(h, t, -0.127414796f);
+  h *= t;                                   // -erfc(x) / 2
+  return fmaf(h * e, a, fmaxf(v, 0.0f));
 }
 
 template <typename T>
@@ -245,41 +214,15 @@ __device__ __forceinline__ void wg_barrier() {
 // s_waitcnt lgkmcnt(0) only.
 #define NSW_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
 
-// Chunk swizzle of a stage row: 64 B (4 chunks) or 128 B (8 chunks).
-template <int ROWB>
+// Chunk swizzle of a 128-byte stage row (8 chunks of 16 bytes).
 __device__ __forceinline__ int row_swizzle(int row) {
   const int r = row & 15;   // position inside the 16-row block
-  if constexpr (ROWB == 64) return ((r >> 1) ^ (r >> 3)) & 3;
-  else return ((r >> 1) & 7) ^ ((r & 1) << 2);
-}
-
-// Copy instruction j of wave w covers stage rows (w*COPIES + j)*RPC .. +RPC-1
-// (x rows first, then w rows), RPC = 1024 / ROWB; lane i writes row
-// +i/(ROWB/16), slot i%(ROWB/16), and therefore loads global chunk
-// slot ^ row_swizzle(row).
-template <int COPIES>
-struct CopyPlan {
-  u32x4 rsrc[COPIES];           // x or w buffer per copy (wave-uniform)
-  uint32_t voff[COPIES];        // byte offset of this lane's chunk at stage 0
-  int lds_row0;                 // first stage row of copy 0 for this wave
-};
-
-// Copy instruction j of stage `st` (k bytes st*ROWB ..) into `stage`.
-template <int COPIES, int ROWB>
-__device__ __forceinline__ void copy_slab(const CopyPlan<COPIES>& cp, char* stage, int j, int st) {
-  dma16(cp.rsrc[j], (uint32_t)(uintptr_t)(stage + (cp.lds_row0 + j * (1024 / ROWB)) * ROWB), cp.voff[j], st * ROWB);
-}
-
-template <int COPIES, int ROWB>
-__device__ __forceinline__ void issue_tile(const CopyPlan<COPIES>& cp, char* stage, int st) {
-#pragma unroll
-  for (int j = 0; j < COPIES; ++j) copy_slab<COPIES, ROWB>(cp, stage, j, st);
+  return ((r >> 1) & 7) ^ ((r & 1) << 2);
 }
 
 // Fragment read: 16 bytes of k chunk `chunk` of a stage row.
-template <int ROWB>
 __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk) {
-  const int slot = chunk ^ row_swizzle<ROWB>(row);
+  const int slot = chunk ^ row_swizzle(row);
   return *reinterpret_cast<const u32x4*>(stage + row * ROWB + slot * 16);
 }
 
@@ -300,7 +243,6 @@ template <typename T, int PRE>
 __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X, const T* __restrict__ Wt, int M,
                                              int N, int K, int m0, int n0, const EpiArgs& ea,
                                              f32x4 (&acc)[8][8], float (&ssr)[8], int wave, int lane) {
-  constexpr int ROWB = 128;               // k bytes per row and stage
   constexpr int SLOT = 256 * ROWB;        // one operand's stage: 32 KB
   constexpr int NC = SLOT / (4 * 1024);   // copies per wave per operand and stage (8)
   constexpr int UNR = 12;                 // steps per loop iteration: 6 stages, a multiple of 3 and 2
@@ -313,7 +255,7 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
     const int srow = wave * 64 + j * 8 + lane / 8;
-    const int chunk = (lane % 8) ^ row_swizzle<ROWB>(srow);
+    const int chunk = (lane % 8) ^ row_swizzle(srow);
     int gx = m0 + srow;
     gx = gx < M ? gx : M - 1;   // rows past the edge re-read the last row (never stored)
     if constexpr (PRE == PRE_ROWNORM_GATHER) gx = (int)ea.geom.token_of_row(gx);
@@ -360,9 +302,9 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
   const int xrow = (wave >> 1) * 128 + frow;   // x rows of this wave (B operand)
   u32x4 fa[2][8], fb[2][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) fa[0][i] = lds_frag<ROWB>(smem + NSW_WSLOT(0), wrow + i * 16, fg);
+  for (int i = 0; i < 8; ++i) fa[0][i] = lds_frag(smem + NSW_WSLOT(0), wrow + i * 16, fg);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) fb[0][i] = lds_frag<ROWB>(smem + NSW_XSLOT(0), xrow + i * 16, fg);
+  for (int i = 0; i < 8; ++i) fb[0][i] = lds_frag(smem + NSW_XSLOT(0), xrow + i * 16, fg);
 
   // step k = kt + U of stage st = k/2; kt is a multiple of UNR, so the slots
   // of the stages touched by step U are compile-time constants
@@ -387,8 +329,8 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
         }                                                                                      \
         /* unconditional: after the last step these read stale slots (unused); a  */         \
         /* conditional read would make the wait-count pass drain all LDS reads   */         \
-        fb[((U) + 1) & 1][mb] = lds_frag<ROWB>(smem + NSW_XSLOT(nsu_), xrow + mb * 16, nsub_ * 4 + fg); \
-        fa[((U) + 1) & 1][mb] = lds_frag<ROWB>(smem + NSW_WSLOT(nsu_), wrow + mb * 16, nsub_ * 4 + fg); \
+        fb[((U) + 1) & 1][mb] = lds_frag(smem + NSW_XSLOT(nsu_), xrow + mb * 16, nsub_ * 4 + fg); \
+        fa[((U) + 1) & 1][mb] = lds_frag(smem + NSW_WSLOT(nsu_), wrow + mb * 16, nsub_ * 4 + fg); \
         _Pragma("unroll") for (int nb = 0; nb < 8; ++nb)                                       \
           mfma_chunk<T>(acc[nb][mb], fa[(U) & 1][nb], fb[(U) & 1][mb]);                        \
         if constexpr (pre_sums_in_loop(PRE)) ssr[mb] = frag_sumsq<T>(fb[(U) & 1][mb], ssr[mb]); \
@@ -410,22 +352,12 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
 #undef NSW_WSLOT
 }
 
-template <typename T, int EPI, int TN, int PRE>
-__global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* __restrict__ X,
-                                                                      const T* __restrict__ Wt,
-                                                                      T* __restrict__ Y, int M, int N,
-                                                                      int K, EpiArgs ea) {
-  constexpr int ROWB = Cfg<TN>::ROWB, SUB = Cfg<TN>::SUB, RPC = Cfg<TN>::RPC, CPG = Cfg<TN>::CPG;
-  constexpr int BN = Cfg<TN>::BN;
-  constexpr int WTN = Cfg<TN>::WTN;
-  constexpr int NB = Cfg<TN>::NB;
-  constexpr int NSTAGE = Cfg<TN>::NSTAGE;
-  constexpr int UNROLL = Cfg<TN>::UNROLL;
-  constexpr int STAGE_BYTES = Cfg<TN>::STAGE_BYTES;
-  constexpr int COPIES = Cfg<TN>::COPIES;
+template <typename T, int EPI, int PRE>
+__global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, const T* __restrict__ Wt,
+                                                     T* __restrict__ Y, int M, int N, int K, EpiArgs ea) {
   // the operand ring during the k loop, the output staging area in the
   // epilogue
-  __shared__ __attribute__((aligned(1024))) char smem[Stg<T, TN>::SMEM];
+  __shared__ __attribute__((aligned(1024))) char smem[Stg<T>::SMEM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -454,111 +386,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   for (int i = 0; i < MB; ++i) ssr[i] = 0.f;
   const int frow = lane & 15, fg = lane >> 4;
 
-  if constexpr (TN == 256) {
-    mainloop_256<T, PRE>(smem, X, Wt, M, N, K, m0, n0, ea, acc, ssr, wave, lane);
-  } else {
-  // ---- copy plan: the stage holds the BM x rows, then the BN w rows
-  const uint32_t rowbytes = (uint32_t)K * sizeof(T);
-  CopyPlan<COPIES> cp;
-  const u32x4 rx = make_rsrc(X, (uint32_t)M * rowbytes);
-  const u32x4 rw = make_rsrc(Wt, (uint32_t)N * rowbytes);
-  cp.lds_row0 = wave * COPIES * RPC;
-  {
-#pragma unroll
-    for (int j = 0; j < COPIES; ++j) {
-      const bool xside = (wave * COPIES + j) * RPC < BM;   // wave-uniform
-      cp.rsrc[j] = xside ? rx : rw;
-      const int srow = cp.lds_row0 + j * RPC + lane / (ROWB / 16);
-      const int chunk = (lane % (ROWB / 16)) ^ row_swizzle<ROWB>(srow);
-      int g = xside ? m0 + srow : n0 + srow - BM;
-      const int lim = xside ? M : N;
-      g = g < lim ? g : lim - 1;   // rows past the edge re-read the last row (never stored)
-      if constexpr (PRE == PRE_ROWNORM_GATHER) {
-        if (xside) g = (int)ea.geom.token_of_row(g);
-      }
-      cp.voff[j] = (uint32_t)g * rowbytes + chunk * 16;
-    }
-  }
-
-  const int arow = BM + wn * WTN + frow;   // w rows of this wave (A operand)
-  const int brow = wm * WTM + frow;        // x rows of this wave (B operand)
-  const int nk = K / (STEPB / (int)sizeof(T));   // MFMA steps
-  const int nst = nk / SUB;                       // LDS stages
-  u32x4 fa[2][NB], fb[2][MB];
-
-#define NSW_STAGE(i) (smem + ((i) % NSTAGE) * STAGE_BYTES)
-#define NSW_WAIT_AHEAD(ahead)                                                                  \
-  do {                                                                                         \
-    const int a_ = (ahead);                                                                    \
-    if (a_ >= 3) NSW_WAIT_VMCNT(3 * COPIES);                                                   \
-    else if (a_ == 2) NSW_WAIT_VMCNT(2 * COPIES);                                              \
-    else if (a_ == 1) NSW_WAIT_VMCNT(COPIES);                                                  \
-    else NSW_WAIT_VMCNT(0);                                                                    \
-  } while (0)
-
-#pragma unroll
-  for (int t = 0; t < NSTAGE; ++t)
-    if (t < nst) issue_tile<COPIES, ROWB>(cp, NSW_STAGE(t), t);
-  NSW_WAIT_AHEAD(min(nst - 1, NSTAGE - 1));
-  wg_barrier();
-#pragma unroll
-  for (int i = 0; i < NB; ++i) fa[0][i] = lds_frag<ROWB>(NSW_STAGE(0), arow + i * 16, fg);
-#pragma unroll
-  for (int i = 0; i < MB; ++i) fb[0][i] = lds_frag<ROWB>(NSW_STAGE(0), brow + i * 16, fg);
-
-#define NSW_STEP(U)                                                                            \
-  {                                                                                            \
-    const int k = kt + U;                                                                      \
-    if (k < nk) {                                                                              \
-      constexpr int su_ = (U) / SUB, sn_ = ((U) + 1) / SUB;                                    \
-      constexpr bool bnd_ = ((U) + 1) % SUB == 0;                                              \
-      constexpr int nch_ = (((U) + 1) % SUB) * 4;                                              \
-      char* const cur = NSW_STAGE(su_);                                                        \
-      if (bnd_ && k + 1 < nk) {                                                                \
-        NSW_WAIT_AHEAD(min(nst - 1, NSTAGE - 1 + k / SUB) - (k + 1) / SUB);                    \
-        NSW_WAIT_LGKMCNT0();                                                                   \
-        wg_barrier();                                                                          \
-      }                                                                                        \
-      /* the next step's stage, also after the last step (a stale, unused read */         \
-      /* that keeps the fragment addresses compile-time offsets)               */         \
-      const char* nx = NSW_STAGE(sn_);                                                         \
-      const int snext = k / SUB + NSTAGE;                                                      \
-      _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                      \
-        if (bnd_ && snext < nst) {                                                             \
-          _Pragma("unroll") for (int c_ = 0; c_ < CPG; ++c_)                                   \
-            if (mb * CPG + c_ < COPIES) copy_slab<COPIES, ROWB>(cp, cur, mb * CPG + c_, snext); \
-        }                                                                                      \
-        fb[(U + 1) & 1][mb] = lds_frag<ROWB>(nx, brow + mb * 16, nch_ + fg);                   \
-        if (mb < NB) fa[(U + 1) & 1][mb] = lds_frag<ROWB>(nx, arow + mb * 16, nch_ + fg);      \
-        _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                      \
-          mfma_chunk<T>(acc[nb][mb], fa[U & 1][nb], fb[U & 1][mb]);                            \
-        if constexpr (pre_sums_in_loop(PRE)) ssr[mb] = frag_sumsq<T>(fb[U & 1][mb], ssr[mb]);  \
-        if (mb < NB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                        \
-        else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                \
-        __builtin_amdgcn_sched_group_barrier(0x008, NB * (sizeof(T) == 2 ? 1 : 4), 0);         \
-      }                                                                                        \
-    }                                                                                          \
-  }
-
-  for (int kt = 0; kt < nk; kt += UNROLL) {
-    NSW_STEP(0)
-    NSW_STEP(1)
-    NSW_STEP(2)
-    NSW_STEP(3)
-    if constexpr (UNROLL >= 6) {
-      NSW_STEP(4)
-      NSW_STEP(5)
-    }
-    if constexpr (UNROLL >= 8) {
-      NSW_STEP(6)
-      NSW_STEP(7)
-    }
-  }
-#undef NSW_STEP
-#undef NSW_WAIT_AHEAD
-#undef NSW_STAGE
-  static_assert(UNROLL % 2 == 0 && UNROLL <= 8, "unroll");
-  }
+  mainloop_256<T, PRE>(smem, X, Wt, M, N, K, m0, n0, ea, acc, ssr, wave, lane);
 
   // ---------------------------------------------------------------- epilogue
   // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
@@ -682,7 +510,7 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   // and residual rows are loaded one batch ahead, the first batch's before
   // the staging writes; the loads use clamped addresses (no branches), only
   // the stores are predicated.
-  using S = Stg<T, TN>;
+  using S = Stg<T>;
   constexpr int VEC = 16 / sizeof(T);                 // elements per 16-byte chunk
   constexpr int LPR = BN / VEC;                       // lanes per output row (32 bf16 / 64 f32)
   constexpr int RPI = 64 / LPR;                       // rows per copy instruction (2 / 1)
@@ -787,14 +615,6 @@ __global__ __launch_bounds__(256, Cfg<TN>::WG_PER_CU) void gemm_kernel(const T* 
   }
 }
 
-template <typename T, int EPI, int TN, int PRE>
-static void launch_tiles(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
-                         const EpiArgs& ea, hipStream_t st) {
-  const int64_t tiles = ((M + BM - 1) / BM) * ((N + TN - 1) / TN);
-  hipLaunchKernelGGL((gemm_kernel<T, EPI, TN, PRE>), dim3((unsigned)tiles), dim3(256), 0, st, (const T*)x,
-                     (const T*)w, (T*)y, (int)M, (int)N, (int)K, ea);
-}
-
 template <typename T, int EPI, int PRE = PRE_NONE>
 static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
                        const EpiArgs& ea, hipStream_t st, const char* what) {
@@ -808,17 +628,10 @@ static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t
   NSW_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)y % 16) == 0 &&
                     ((uintptr_t)ea.residual % 16) == 0,
                 "%s: x, w, y and residual must be 16-byte aligned", what);
-  NSW_CHECK_ARG(((M + BM - 1) / BM) * ((N + 127) / 128) < (1LL << 31), "%s: too many tiles", what);
-  // Short K with the GELU epilogue (~23 VALU slots per output): 256x128, two
-  // workgroups per CU overlap one tile's epilogue with the other's MFMAs.
-  // Otherwise (head norm and row scatter included, measured faster there)
-  // the 256x256 main loop.
-  if constexpr (EPI == EPI_BIAS_GELU) {
-    if (K <= 2048) launch_tiles<T, EPI, 128, PRE>(x, w, y, M, N, K, ea, st);
-    else launch_tiles<T, EPI, 256, PRE>(x, w, y, M, N, K, ea, st);
-  } else {
-    launch_tiles<T, EPI, 256, PRE>(x, w, y, M, N, K, ea, st);
-  }
+  NSW_CHECK_ARG(((M + BM - 1) / BM) * ((N + BN - 1) / BN) < (1LL << 31), "%s: too many tiles", what);
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  hipLaunchKernelGGL((gemm_kernel<T, EPI, PRE>), dim3((unsigned)tiles), dim3(256), 0, st, (const T*)x, (const T*)w,
+                     (T*)y, (int)M, (int)N, (int)K, ea);
   return check_launch(what);
 }
 
