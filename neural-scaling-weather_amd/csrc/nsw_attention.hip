@@ -14,7 +14,9 @@
 //      O^T = V^T P^T (the k order of a 32-key step is {4g+r, 16+4g+r} for lane
 //      group g; V^T is stored with its keys in that order, so each A fragment
 //      is one 16-byte LDS read), and
-//   4. writes O[q][h*hd + d] with one 8-byte store per 4 head dims.
+//   4. writes O[q][h*hd + d] in 16-byte chunks (lane pairs exchange halves
+//      with v_permlane16_swap).
+// Workgroup ids are remapped so that the heads of a window share one XCD.
 // Padding keys get -inf logits; no FLOPs are counted for them.
 //
 // Generic path (attn_scalar_kernel, fp32 and any head dim): one thread per
@@ -78,6 +80,7 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
   constexpr int VT_STRIDE = KP + 8;                // bf16 elements per V^T row (4 banks mod 64 dwords)
   constexpr int NS = HD / 32;                      // k-steps of the QK^T product
   constexpr int NDB = HD / 16;                     // 16-wide head-dim blocks
+  static_assert(NDB % 2 == 0, "output stores pair 16-wide head-dim blocks");
   constexpr int NKS = KP / 32;                     // 32-key steps of PV
   constexpr int CPR = HD / 8;                      // 16-byte chunks per K / V row
   constexpr int NCH = (KP * CPR + 255) / 256;      // chunks staged per thread
@@ -87,8 +90,11 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 Vt[HD * VT_STRIDE];
   __shared__ uint64_t cls[NCLS];
 
-  const int win = (int)(blockIdx.x / (unsigned)a.heads);
-  const int head = (int)blockIdx.x - win * a.heads;
+  // The heads of a window run on one XCD at about the same time, so that the
+  // window's qkv rows and output rows are read and written whole there.
+  const int item = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int win = item / a.heads;
+  const int head = item - win * a.heads;
   const int L = a.L, C = a.C;
   const int64_t ld = 3 * (int64_t)C;
   const bf16* base = (const bf16*)a.qkv + (int64_t)win * L * ld + head * HD;
@@ -247,14 +253,31 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
       }
       Z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, Z, 0, 0, 0);
     }
-    if (q < L) {
-      const float inv = 1.0f / Z[0];
-      bf16* orow = (bf16*)a.o + ((int64_t)win * L + q) * (int64_t)C + head * HD;
+    // Lane (fr, fg) holds dims 16 db + 4 fg .. +3 of query fr.  A
+    // v_permlane16_swap of (db = 2j, db = 2j+1) pairs lane groups fg = 2m and
+    // 2m+1: afterwards the even group holds dims 16 db + 8m .. +7 of db = 2j
+    // and the odd group those of db = 2j+1, so every lane writes 16 B chunks.
+    const float inv = 1.0f / Z[0];
+    float lo[NDB / 2][2], hi[NDB / 2][2];
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        float v[4] = {O[db][0] * inv, O[db][1] * inv, O[db][2] * inv, O[db][3] * inv};
-        store4<bf16>(orow + db * 16 + 4 * fg, v);
+    for (int j = 0; j < NDB / 2; ++j) {
+      const bf16x4 e = {(bf16)(O[2 * j][0] * inv), (bf16)(O[2 * j][1] * inv), (bf16)(O[2 * j][2] * inv),
+                        (bf16)(O[2 * j][3] * inv)};
+      const bf16x4 f = {(bf16)(O[2 * j + 1][0] * inv), (bf16)(O[2 * j + 1][1] * inv),
+                        (bf16)(O[2 * j + 1][2] * inv), (bf16)(O[2 * j + 1][3] * inv)};
+      const f32x2 ev = __builtin_bit_cast(f32x2, e), fv = __builtin_bit_cast(f32x2, f);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        lo[j][h] = ev[h];
+        hi[j][h] = fv[h];
+        permlane16_swap(lo[j][h], hi[j][h]);
       }
+    }
+    if (q < L) {
+      bf16* orow = (bf16*)a.o + ((int64_t)win * L + q) * (int64_t)C + head * HD + 8 * (fg >> 1) + 16 * (fg & 1);
+#pragma unroll
+      for (int j = 0; j < NDB / 2; ++j)
+        *reinterpret_cast<f32x4*>(orow + 32 * j) = f32x4{lo[j][0], lo[j][1], hi[j][0], hi[j][1]};
     }
   }
 }

@@ -148,6 +148,17 @@ __device__ __forceinline__ float rows4_max(float x) {
   return fmaxf(c, d);
 }
 
+// ------------------------------------------------------- XCD placement ----
+// Workgroups are dispatched round-robin over the 8 XCDs (XCD x receives ids
+// x, x+8, x+16, ...), each with its own L2.  This bijection over [0, n) gives
+// XCD x the contiguous logical range [x*q + min(x, rem), ...), q = n / 8,
+// rem = n % 8, so that neighbouring logical items share one L2.
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  const int q = n >> 3, rem = n & 7;
+  const int x = bid & 7, idx = bid >> 3;
+  return x * q + (x < rem ? x : rem) + idx;
+}
+
 // ------------------------------------------------- division by a constant ---
 // Exact unsigned 32-bit division by a divisor fixed when a kernel is launched
 // (Granlund & Montgomery, "Division by invariant integers using

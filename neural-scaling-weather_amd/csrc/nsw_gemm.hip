@@ -168,16 +168,8 @@ __device__ __forceinline__ float frag_sumsq(const u32x4& f, float s) {
   return s;
 }
 
-// Bijective remap of the hardware workgroup id so that XCD x (which receives
-// ids x, x+8, x+16, ...) processes the contiguous logical range
-// [x*q + min(x, rem), ...); GROUP_M row blocks per tile group.
+// Row blocks per tile group of one XCD (tiles come from xcd_remap).
 constexpr int GROUP_M = 8;
-
-__device__ __forceinline__ int xcd_remap(int bid, int ntiles) {
-  const int q = ntiles >> 3, rem = ntiles & 7;
-  const int x = bid & 7, idx = bid >> 3;
-  return x * q + (x < rem ? x : rem) + idx;
-}
 
 // Buffer resource (V#) over a whole tensor: raw buffer, stride 0, 32-bit
 // byte offsets, num_records = bytes, dword 3 = 0x00020000 (the gfx9 raw
