@@ -72,11 +72,30 @@ __device__ __forceinline__ int vt_pos(int k) {
   return (k & ~31) | ((j & 15) >> 2) << 3 | (j >> 4) << 2 | (j & 3);
 }
 
+// 16-byte chunk slot of chunk ch in K row r (SW: 8 chunks per row, XOR
+// swizzle ((r >> 1) & 7) ^ ((r & 1) << 2): the 16 rows of a fragment read, or
+// two rows of 8 chunks in a staging write, cover all banks once whether LDS
+// serves 16 lanes over 64 banks or 8 lanes over 32).  Depends on r mod 16
+// only, so a fragment row fr can stand for kb * 16 + fr.
+template <bool SW>
+__device__ __forceinline__ int k_chunk(int r, int ch) { return SW ? ch ^ (((r >> 1) & 7) ^ ((r & 1) << 2)) : ch; }
+
+// LDS row of head dim d in V^T: within each group of 8 dims the rows are
+// rotated by the group index, so that the staging writes of one instruction
+// (lane = 16-byte chunk ch of a key row, element e: dim 8 ch + e) land in
+// different banks; a fragment read (16 consecutive dims) still covers 16
+// distinct rows of the same 8-row groups, conflict-free as before.
+__device__ __forceinline__ int vt_row(int d) { return (d & ~7) | ((d + (d >> 3)) & 7); }
+
 // NKB = ceil(L / 16) exactly, so only the last 16-key block holds padding.
 template <int HD, int NKB, bool MT>
 __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
   constexpr int KP = ((NKB * 16 + 31) / 32) * 32;  // padded keys (multiple of 32)
-  constexpr int KS_STRIDE = HD + 8;                // bf16 elements per K row in LDS
+  // 128-byte K rows (hd 64) are stored unpadded with XOR-swizzled 16-byte
+  // chunks (conflict-free staging writes and fragment reads); 64-byte rows
+  // (hd 32) are padded by 16 bytes
+  constexpr bool KSW = HD == 64;
+  constexpr int KS_STRIDE = KSW ? HD : HD + 8;     // bf16 elements per K row in LDS
   constexpr int VT_STRIDE = KP + 8;                // bf16 elements per V^T row (4 banks mod 64 dwords)
   constexpr int NS = HD / 32;                      // k-steps of the QK^T product
   constexpr int NDB = HD / 16;                     // 16-wide head-dim blocks
@@ -134,10 +153,10 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
     const int idx = tid + 256 * c;
     const int key = idx / CPR, ch = idx - key * CPR;
     if (idx < KP * CPR) {
-      *reinterpret_cast<bf16x8*>(&Ks[key * KS_STRIDE + ch * 8]) = kv[c];
+      *reinterpret_cast<bf16x8*>(&Ks[key * KS_STRIDE + k_chunk<KSW>(key, ch) * 8]) = kv[c];
       const int kpos = vt_pos(key);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[(ch * 8 + e) * VT_STRIDE + kpos] = vv[c][e];
+      for (int e = 0; e < 8; ++e) Vt[vt_row(ch * 8 + e) * VT_STRIDE + kpos] = vv[c][e];
     }
   }
   // Shift mask of a last-band window: key class = (row within the window)
@@ -173,7 +192,7 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
     for (int kb = 0; kb < KD; ++kb)
 #pragma unroll
       for (int s = 0; s < NS; ++s)
-        kf[kb][s] = *reinterpret_cast<const bf16x8*>(&Ks[(kb * 16 + fr) * KS_STRIDE + 32 * s + 8 * fg]);
+        kf[kb][s] = *reinterpret_cast<const bf16x8*>(&Ks[(kb * 16 + fr) * KS_STRIDE + k_chunk<KSW>(fr, 4 * s + fg) * 8]);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -182,8 +201,8 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
       if (kb + KD < NKB) {
 #pragma unroll
         for (int s = 0; s < NS; ++s)
-          kf[kb % KD][s] =
-              *reinterpret_cast<const bf16x8*>(&Ks[((kb + KD) * 16 + fr) * KS_STRIDE + 32 * s + 8 * fg]);
+          kf[kb % KD][s] = *reinterpret_cast<const bf16x8*>(
+              &Ks[((kb + KD) * 16 + fr) * KS_STRIDE + k_chunk<KSW>(fr, 4 * s + fg) * 8]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -235,7 +254,7 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
     auto load_v = [&](int buf, int ks) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
-        vf[buf][db] = *reinterpret_cast<const bf16x8*>(&Vt[(db * 16 + fr) * VT_STRIDE + 32 * ks + 8 * fg]);
+        vf[buf][db] = *reinterpret_cast<const bf16x8*>(&Vt[vt_row(db * 16 + fr) * VT_STRIDE + 32 * ks + 8 * fg]);
     };
     load_v(0, 0);
 #pragma unroll
