@@ -267,7 +267,7 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
 
   const int nk = K / (STEPB / (int)sizeof(T));   // MFMA steps
   const int nst = nk / 2;                          // stages
-  // prologue: x0 w0 x1 w1 x2, then wait for x0 and w0
+  // prologue: x0 w0 x1 w1, then wait for x0 and w0 (step 0 issues x2)
 #pragma unroll
   for (int j = 0; j < NC; ++j) NSW_COPY_X(0, 0, j);
 #pragma unroll
@@ -277,12 +277,6 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
     for (int j = 0; j < NC; ++j) NSW_COPY_X(1, 1, j);
 #pragma unroll
     for (int j = 0; j < NC; ++j) NSW_COPY_W(1, 1, j);
-  }
-  if (nst > 2) {
-#pragma unroll
-    for (int j = 0; j < NC; ++j) NSW_COPY_X(2, 2, j);
-    NSW_WAIT_VMCNT(3 * NC);
-  } else if (nst > 1) {
     NSW_WAIT_VMCNT(2 * NC);
   } else {
     NSW_WAIT_VMCNT(0);
@@ -299,7 +293,15 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
   for (int i = 0; i < 8; ++i) fb[0][i] = lds_frag(smem + NSW_XSLOT(0), xrow + i * 16, fg);
 
   // step k = kt + U of stage st = k/2; kt is a multiple of UNR, so the slots
-  // of the stages touched by step U are compile-time constants
+  // of the stages touched by step U are compile-time constants.  Step k
+  // copies stage st + 2 (x in its first step, w in its second) with no
+  // condition: uniform branches around the copies cost ~7% of the loop.  Past
+  // the last stage these copies read rows beyond k (or zeros past the end of
+  // the buffer) into slots nothing reads: x into the slot of stage st - 1,
+  // w into the slot of stage st, which the barrier at the start of the step
+  // has freed, except in the last step (no barrier): its w copies go to the
+  // x slot of stage st + 1, unused.  The epilogue drains them before it
+  // writes LDS.
 #define NSW_STEP256(U)                                                                         \
   {                                                                                            \
     const int k = kt + U;                                                                      \
@@ -308,17 +310,14 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
       constexpr int nsub_ = ((U) + 1) % 2, nsu_ = ((U) + 1) / 2;                               \
       const int st = k >> 1;                                                                   \
       if (sub_ == 1 && k + 1 < nk) {                                                           \
-        if (st + 2 < nst) NSW_WAIT_VMCNT(NC);                                                  \
-        else NSW_WAIT_VMCNT(0);                                                                \
+        NSW_WAIT_VMCNT(NC);                                                                    \
         NSW_WAIT_LGKMCNT0();                                                                   \
         wg_barrier();                                                                          \
       }                                                                                        \
-      const bool cp_ = sub_ == 1 ? st + 2 < nst : (k >= 2 && st + 2 < nst);                    \
+      const uint32_t wdst_ = cbase + (k + 1 < nk ? NSW_WSLOT(su_ + 2) : NSW_XSLOT(su_ + 1));    \
       _Pragma("unroll") for (int mb = 0; mb < 8; ++mb) {                                       \
-        if (cp_) {                                                                             \
-          if (sub_ == 1) NSW_COPY_W(su_ + 2, st + 2, mb);                                      \
-          else NSW_COPY_X(su_ + 2, st + 2, mb);                                                \
-        }                                                                                      \
+        if (sub_ == 1) dma16(rw, wdst_ + mb * 1024, vw[mb], (st + 2) * ROWB);                  \
+        else NSW_COPY_X(su_ + 2, st + 2, mb);                                                  \
         /* unconditional: after the last step these read stale slots (unused); a  */         \
         /* conditional read would make the wait-count pass drain all LDS reads   */         \
         fb[((U) + 1) & 1][mb] = lds_frag(smem + NSW_XSLOT(nsu_), xrow + mb * 16, nsub_ * 4 + fg); \
@@ -512,6 +511,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
   static_assert(ITER % BATCH == 0, "batch");
   constexpr bool RES = EPI == EPI_BIAS_RESIDUAL || EPI == EPI_SCATTER_RESIDUAL;
   constexpr bool SCAT = EPI == EPI_SCATTER_RESIDUAL;
+  NSW_WAIT_VMCNT(0);                                  // the copies past the last stage
   NSW_WAIT_LGKMCNT0();
   wg_barrier();                                       // the operand ring is no longer read
   char* stg = smem;
