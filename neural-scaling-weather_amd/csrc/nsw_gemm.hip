@@ -296,8 +296,8 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
   // of the stages touched by step U are compile-time constants.  Step k
   // copies stage st + 2 (x in its first step, w in its second) with no
   // condition: uniform branches around the copies cost ~7% of the loop.  Past
-  // the last stage these copies read rows beyond k (or zeros past the end of
-  // the buffer) into slots nothing reads: x into the slot of stage st - 1,
+  // the last stage these copies re-read the last stage (L2-resident) into
+  // slots nothing reads: x into the slot of stage st - 1,
   // w into the slot of stage st, which the barrier at the start of the step
   // has freed, except in the last step (no barrier): its w copies go to the
   // x slot of stage st + 1, unused.  The epilogue drains them before it
@@ -315,9 +315,10 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
         wg_barrier();                                                                          \
       }                                                                                        \
       const uint32_t wdst_ = cbase + (k + 1 < nk ? NSW_WSLOT(su_ + 2) : NSW_XSLOT(su_ + 1));    \
+      const int cst_ = st + 2 < nst ? st + 2 : nst - 1;   /* past the end: the last stage, in L2 */ \
       _Pragma("unroll") for (int mb = 0; mb < 8; ++mb) {                                       \
-        if (sub_ == 1) dma16(rw, wdst_ + mb * 1024, vw[mb], (st + 2) * ROWB);                  \
-        else NSW_COPY_X(su_ + 2, st + 2, mb);                                                  \
+        if (sub_ == 1) dma16(rw, wdst_ + mb * 1024, vw[mb], cst_ * ROWB);                      \
+        else NSW_COPY_X(su_ + 2, cst_, mb);                                                    \
         /* unconditional: after the last step these read stale slots (unused); a  */         \
         /* conditional read would make the wait-count pass drain all LDS reads   */         \
         fb[((U) + 1) & 1][mb] = lds_frag(smem + NSW_XSLOT(nsu_), xrow + mb * 16, nsub_ * 4 + fg); \
