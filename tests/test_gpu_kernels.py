@@ -62,6 +62,11 @@ GEMM_SHAPES = [
     (300, 192, 768),
     (257, 4096, 256),
     (16, 64, 64),
+    # stage counts around the main loop's 12-step iterations (the operand
+    # copies past the last stage land in unused LDS slots): 2, 7 and 5 stages
+    (96, 128, 128),
+    (513, 320, 448),
+    (64, 256, 320),
 ]
 
 
