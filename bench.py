@@ -35,6 +35,7 @@ for _p in (ROOT, os.path.join(ROOT, "neural-scaling-weather_amd")):
         sys.path.insert(0, _p)
 
 METRIC = "Swin-block fwd tokens/s + % MFMA/HBM roofline, p4 e1024 180x360, 1 GPU"
+SPIN_CYCLES = 400_000     # ~0.2 ms spin before diagnostic event sequences
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_F32_TFLOPS = 157.3     # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
@@ -188,6 +189,10 @@ def main():
         times = {n: [] for n in names}
         for it in range(args.warmup + args.steps):
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+            # a short spin kernel ahead of the first event keeps the GPU busy
+            # while the host enqueues the first op, so that op's interval
+            # holds its kernel and not the host's launch latency
+            torch.cuda._sleep(SPIN_CYCLES)
             ev[0].record(stream)
             for i, (_, fn) in enumerate(seq):
                 fn()
@@ -316,8 +321,9 @@ def model_sections(dev, steps, warmup, with_rollout=True):
         e1.record(stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
-        # stage split
+        # stage split (spin kernel first: see the per-kernel loop of the block)
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        torch.cuda._sleep(SPIN_CYCLES)
         ev[0].record(stream)
         tok = model.prepare_tokens(x)
         ev[1].record(stream)
