@@ -96,6 +96,14 @@ template <typename T> struct Stg {
   static constexpr int SMEM = RING > BYTES ? RING : BYTES;
   static_assert(SMEM <= LDS_BUDGET, "LDS use exceeds the CU's 160 KB");
 };
+// LDS floats at PARAM_LDS take the epilogue's parameters (above the staging
+// rows of either dtype): bias [0, 256), q/k norm weights [PRM_NW, +128), row
+// scales [PRM_RS, +256).
+constexpr int PARAM_LDS = 140 * 1024;
+constexpr int PRM_NW = 256, PRM_RS = 384;
+static_assert(Stg<bf16>::BYTES <= PARAM_LDS && Stg<float>::BYTES <= PARAM_LDS &&
+              PARAM_LDS + (PRM_RS + 256) * 4 <= RING, "epilogue parameters in LDS");
+
 
 struct EpiArgs {
   const void* bias;
@@ -384,6 +392,14 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
   // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
   //                                          [n0 + wn*WTN + nb*16 + 4*fg + r]
   const int nw0 = n0 + wn * WTN;           // first column of this wave
+  constexpr int HDQ = qkv_head_dim(EPI);
+  // With the head norm or the row scale, the bias, norm weights and row
+  // scales reach the lanes through LDS (one element per thread, parked there
+  // once the operand ring is free): loaded straight into the fragment layout,
+  // their 16+ small loads went out one at a time, each behind the previous
+  // one, because the accumulators copied out of the AGPRs fill the VGPRs
+  // here.  The bias-only epilogues load it directly (one batch).
+  constexpr bool PLDS = HDQ > 0 || PRE == PRE_ROWSCALE;
   const T* bias = (const T*)ea.bias;
   float bv[NB][4];
 #pragma unroll
@@ -391,16 +407,16 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
     const int n = nw0 + nb * 16 + fg * 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) bv[nb][r] = 0.f;
-    if constexpr (EPI != EPI_NONE) load4<T>(bias + (n < N ? n : 0), bv[nb]);   // straight-line: one batch
+    if constexpr (EPI != EPI_NONE && !PLDS) load4<T>(bias + (n < N ? n : 0), bv[nb]);   // straight-line: one batch
   }
 
   // per-head RMSNorm (QKV epilogue): a head is HDQ/16 consecutive 16-column
   // blocks inside one of the q / k / v regions (C % 64 == 0, HDQ | 64), so
   // whether a head is normalised is uniform across the wave
-  constexpr int HDQ = qkv_head_dim(EPI);
   constexpr int NBH = HDQ > 0 ? HDQ / 16 : 1;   // blocks per head
   constexpr int NHW = NB / NBH;                 // heads per wave tile
   bool normed[NHW];
+  int nwreg[NHW];                               // 0: q weights, 1: k weights
   float nwv[NB][4];
   if constexpr (HDQ > 0) {
 #pragma unroll
@@ -408,10 +424,35 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
       const int c0 = nw0 + h * HDQ;
       const int region = c0 / ea.C;  // 0: q, 1: k, 2: v
       normed[h] = region < 2 && c0 < N;
-      const T* nwp = (const T*)(region == 0 ? ea.qn_w : ea.kn_w);
-#pragma unroll
-      for (int b = 0; b < NBH; ++b) load4<T>(nwp + b * 16 + fg * 4, nwv[h * NBH + b]);   // used only if normed
+      nwreg[h] = region == 0 ? 0 : 1;
     }
+  }
+
+  // this thread's parameter element, loaded here and parked in LDS once the
+  // operand ring is free (see the write-out)
+  float p_bias = 0.f, p_nw = 0.f, p_rs = 1.f;
+  if constexpr (EPI != EPI_NONE && PLDS) {
+    const int n = n0 + tid;
+    p_bias = n < N ? to_f32(((const T*)ea.bias)[n]) : 0.f;
+  }
+  if constexpr (HDQ > 0) {
+    if (tid < 2 * HDQ) p_nw = to_f32(((const T*)(tid < HDQ ? ea.qn_w : ea.kn_w))[tid % HDQ]);
+  }
+  if constexpr (PRE == PRE_ROWSCALE) {
+    // row m0 + tid's norm from the producer's partial sums of squares, added
+    // in a fixed order (rows past M read row 0 and are never stored)
+    const int m = m0 + tid;
+    const float* pp = ea.row_sumsq + (int64_t)(m < M ? m : 0) * ea.nparts;
+    float ss = 0.f;
+    int q = 0;
+    if ((ea.nparts & 3) == 0) {
+      for (; q < ea.nparts; q += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(pp + q);
+        ss += (v[0] + v[1]) + (v[2] + v[3]);
+      }
+    }
+    for (; q < ea.nparts; ++q) ss += pp[q];
+    p_rs = 1.0f / sqrtf(ss / (float)K + ea.eps);
   }
 
   // PRE: the four lane groups hold the four k chunks of each x row
@@ -421,38 +462,6 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
     rsr[mb] = 1.f;
     if constexpr (pre_sums_in_loop(PRE)) rsr[mb] = 1.0f / sqrtf(rows4_sum(ssr[mb]) / (float)K + ea.eps);
   }
-  if constexpr (PRE == PRE_ROWSCALE) {
-    // the producer's partial sums of this lane's MB x rows, read as one batch
-    // of loads per 4 partials (rows past M read row 0 and are never stored)
-    const float* pp[MB];
-    float ss[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int m = m0 + wm * WTM + mb * 16 + frow;
-      pp[mb] = ea.row_sumsq + (int64_t)(m < M ? m : 0) * ea.nparts;
-      ss[mb] = 0.f;
-    }
-    int q = 0;
-    if ((ea.nparts & 3) == 0) {
-      for (; q < ea.nparts; q += 4) {
-        f32x4 v[MB];
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) v[mb] = *reinterpret_cast<const f32x4*>(pp[mb] + q);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) ss[mb] += (v[mb][0] + v[mb][1]) + (v[mb][2] + v[mb][3]);
-      }
-    }
-    for (; q < ea.nparts; ++q) {
-      float v[MB];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) v[mb] = pp[mb][q];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) ss[mb] += v[mb];
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) rsr[mb] = 1.0f / sqrtf(ss[mb] / (float)K + ea.eps);
-  }
-
   // 1. epilogue math of row block mb in the fragment layout (bias, row scale,
   // head norm, GELU), evaluated where the block is staged
   auto row_values = [&](int mb, float (&v)[NB][4]) {
@@ -515,6 +524,39 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
   NSW_WAIT_VMCNT(0);                                  // the copies past the last stage
   NSW_WAIT_LGKMCNT0();
   wg_barrier();                                       // the operand ring is no longer read
+  if constexpr (PLDS) {
+    // epilogue parameters, one element per thread: the tile's 256 bias
+    // values, the q and k norm weights, the 256 row scales
+    float* prm = reinterpret_cast<float*>(smem + PARAM_LDS);
+    if constexpr (EPI != EPI_NONE) prm[tid] = p_bias;
+    if constexpr (HDQ > 0) {
+      if (tid < 2 * HDQ) prm[PRM_NW + tid] = p_nw;
+    }
+    if constexpr (PRE == PRE_ROWSCALE) prm[PRM_RS + tid] = p_rs;
+    NSW_WAIT_LGKMCNT0();
+    wg_barrier();
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const f32x4 b4 = EPI != EPI_NONE ? *reinterpret_cast<const f32x4*>(prm + wn * WTN + nb * 16 + fg * 4)
+                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bv[nb][r] = b4[r];
+    }
+    if constexpr (HDQ > 0) {
+#pragma unroll
+      for (int h = 0; h < NHW; ++h)
+#pragma unroll
+        for (int b = 0; b < NBH; ++b) {
+          const f32x4 w4 = *reinterpret_cast<const f32x4*>(prm + PRM_NW + nwreg[h] * HDQ + b * 16 + fg * 4);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) nwv[h * NBH + b][r] = w4[r];
+        }
+    }
+    if constexpr (PRE == PRE_ROWSCALE) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) rsr[mb] = prm[PRM_RS + wm * WTM + mb * 16 + frow];
+    }
+  }
   char* stg = smem;
   const int lrow = lane / LPR;                        // row of this lane within an instruction
   const int col = (lane % LPR) * VEC;                 // first tile column of this lane
