@@ -133,6 +133,39 @@ def test_model_fp32(device, B, T, C_in, C_out, H, W, p, E, heads, ws, depth, coo
     assert rel_l2(model.forward_head(tok), mr.forward_head(tw, prm["head.weight"], p, C_out)) < 1e-6
 
 
+def test_model_from_te_checkpoint_fp32(device, tmp_path):
+    """A whole-model checkpoint in the production layout (TE block names, DDP
+    and TimeStepper prefixes, a TE _extra_state entry; models/helpers.py:53-70,
+    tests/test_te.py:34-71) written to disk, read back with the safe loader
+    into a freshly initialised model and run on the GPU matches the oracle
+    forward of the parameters that were saved."""
+    import nsw
+    from nsw import checkpoint
+    B, T, C_in, C_out, H, W, p, E, heads, ws, depth, coord = MODEL_CASES[0]
+    lat = torch.linspace(90, -90, H + 1)[:-1]
+    lon = torch.linspace(0, 360, W + 1)[:-1]
+    sp = mr.spatial_coords(lat, lon)
+    meta = {"coords": sp, "sp_shapes": [[H], [W]], "n_channels": C_out}
+    model = nsw.SwinTransformer(temporal_context_window_size=T, window_size=ws, patch_size=p, in_chans=C_in,
+                                out_chans=C_out, embed_dim=E, depth=depth, num_heads=heads, coord_pos_embed=coord,
+                                domain_metadata=meta)
+    prm = synth.model_params(C_in, C_out, E, depth, heads, p, seed=23, coord_pos_embed=coord,
+                             pos_shape=(1, T, H // p, W // p, E), random_bias=True, random_norm=True)
+    state = {"module.model." + k: v for k, v in checkpoint.vanilla_to_te(prm).items()}
+    state["module.model.blocks.1.rms_norm_mlp._extra_state"] = torch.zeros(4)
+    path = tmp_path / "ckpt_best.tar"
+    torch.save({"model_state": state, "epoch": 7}, path)
+    missing, unexpected = model.load_state_dict(checkpoint.load_checkpoint_model_state(str(path)), strict=False)
+    assert not unexpected and not [k for k in missing if not k.endswith("attn_mask")], (missing, unexpected)
+    model = model.to(device)
+    x = synth.activations((B, T, C_in, H, W), seed=29)
+    want = mr.model_forward(x, prm, patch_size=p, window_size=ws, depth=depth, num_heads=heads,
+                            out_chans=C_out, coords=mr.model_coords(sp, T) if coord else None)
+    got = model(x.to(device))
+    assert got.shape == (B, 1, C_out, H, W)
+    assert rel_l2(got, want) < 1e-5
+
+
 BF16_CASES = [
     # bf16 MFMA attention head dims (32, 64)
     (2, 2, 6, 6, 36, 72, 2, 128, 4, (9, 18), 2, True),

@@ -115,3 +115,18 @@ def test_full_model_te_checkpoint_loads_into_swin_transformer(tmp_path):
     assert set(sd) == set(prm)
     for k, v in prm.items():
         assert torch.equal(sd[k], v), k
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 exits (status 2) with one JSON line that
+    says the build runs on one GPU, before it initialises any device."""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], cwd=root,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2, r.stderr
+    line = json.loads(r.stdout.strip().splitlines()[-1])
+    assert line["n_gpus"] == 2 and "one GPU" in line["error"]
