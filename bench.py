@@ -102,7 +102,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the Swin block path has no "
-                                   "multi-GPU mode here (see DESIGN.md for how it would shard)",
+                                   "multi-GPU mode here; run with --gpus 1 (the value is one GPU's throughput)",
                           "n_gpus": args.gpus}), flush=True)
         sys.exit(2)
 
