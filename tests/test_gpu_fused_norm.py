@@ -42,7 +42,7 @@ CASES = [
 def test_qkv_projection_norm_gather(device, dtype, B, T, H, W, C, heads, ws, shift):
     from nsw import ops
     M = B * T * H * W
-    if dtype == torch.float32 and M * C * C * 3 > 1e11:
+    if dtype == torch.float32 and M * C * C * 3 > 3e11:
         pytest.skip("fp32 CPU oracle too slow at this size")
     hd = C // heads
     g = torch.Generator().manual_seed(C + H)
@@ -77,7 +77,7 @@ def test_qkv_projection_norm_gather(device, dtype, B, T, H, W, C, heads, ws, shi
 @pytest.mark.parametrize("epi", ["none", "bias", "gelu", "residual"])
 def test_linear_rownorm(device, dtype, M, N, K, epi):
     from nsw import _lib, ops
-    if dtype == torch.float32 and M * N * K > 2e10:
+    if dtype == torch.float32 and M * N * K > 3e11:
         pytest.skip("fp32 CPU oracle too slow at this size")
     g = torch.Generator().manual_seed(M + N + K)
     x = (2.0 * torch.randn(M, K, generator=g) - 0.3).to(dtype)
@@ -148,7 +148,7 @@ def test_proj_reverse_residual_sumsq(device, dtype, B, T, H, W, C, ws, shift):
 @pytest.mark.parametrize("epi", ["none", "gelu", "residual"])
 def test_linear_rowscale(device, dtype, M, N, K, epi):
     from nsw import _lib, ops
-    if dtype == torch.float32 and M * N * K > 2e10:
+    if dtype == torch.float32 and M * N * K > 3e11:
         pytest.skip("fp32 CPU oracle too slow at this size")
     g = torch.Generator().manual_seed(M + N + K + 7)
     x = (2.0 * torch.randn(M, K, generator=g) - 0.3).to(dtype)

@@ -75,7 +75,7 @@ GEMM_SHAPES = [
 @pytest.mark.parametrize("epi", ["none", "bias", "gelu", "residual"])
 def test_linear_epilogues(device, dtype, M, N, K, epi):
     from nsw import _lib, ops
-    if dtype == torch.float32 and M * N * K > 2e10:
+    if dtype == torch.float32 and M * N * K > 1e11:
         pytest.skip("fp32 CPU oracle too slow at this size")
     g = torch.Generator().manual_seed(M + N + K)
     x = torch.randn(M, K, generator=g).to(dtype)
@@ -105,7 +105,7 @@ def test_linear_epilogues(device, dtype, M, N, K, epi):
 @pytest.mark.parametrize("M,C,heads", [(64800, 1024, 16), (16200, 192, 6), (500, 128, 8), (100, 64, 1)])
 def test_qkv_projection_headnorm(device, dtype, M, C, heads):
     from nsw import ops
-    if dtype == torch.float32 and M * C * C * 3 > 1e11:
+    if dtype == torch.float32 and M * C * C * 3 > 3e11:
         pytest.skip("fp32 CPU oracle too slow at this size")
     hd = C // heads
     g = torch.Generator().manual_seed(7)
