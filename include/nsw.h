@@ -42,6 +42,9 @@ extern "C" {
 #define NSW_EPI_BIAS 1          /* y = x W^T + b                               */
 #define NSW_EPI_BIAS_GELU 2     /* y = gelu_erf(x W^T + b)                     */
 #define NSW_EPI_BIAS_RESIDUAL 3 /* y = x W^T + b + residual                    */
+#define NSW_EPI_BIAS_GELU_TANH 4 /* y = gelu_tanh(x W^T + b): the tanh-form GELU of
+                                    the reference's TE block ("gelu" activation of
+                                    te.LayerNormMLP, models/swin_helpers_te.py:318-323) */
 
 const char* nsw_last_error(void);
 int nsw_version(void);
@@ -93,6 +96,12 @@ int nsw_selftest_fastdiv(void);
  * y = x * rsqrt(mean(x^2) + eps) * w, rows x C. */
 int nsw_rmsnorm(const void* x, const void* w, float eps, void* y, int64_t rows, int64_t C,
                 int dtype, void* stream);
+
+/* nn.LayerNorm over the last dim (NormLayer with norm_type="layer_norm",
+ * models/layer_helpers.py:94-100,118-119): y = (x - mean) / sqrt(var + eps)
+ * * w + b, biased variance, rows x C; w and b may be NULL (no affine). */
+int nsw_layernorm(const void* x, const void* w, const void* b, float eps, void* y, int64_t rows,
+                  int64_t C, int dtype, void* stream);
 
 /* Fused norm1 + cyclic roll by -shift + window_partition
  * (models/swin_helpers.py:446 + :402-412): x [B,T,H,W,C] -> xw [B*nW*T*wa, C]. */
@@ -184,6 +193,8 @@ typedef struct nsw_block_shape {
   int64_t hidden;          /* MLP hidden features = int(C * mlp_ratio)          */
   float eps;               /* RMSNorm eps (nn.RMSNorm eps=None: finfo(dtype).eps)*/
   int dtype;
+  int gelu_tanh;           /* 0: exact-erf GELU (nn.GELU(), models/mlp.py:55);  */
+                           /* 1: tanh form (the TE block's "gelu")              */
 } nsw_block_shape;
 
 /* Bytes of device workspace nsw_swin_block_forward needs. */
@@ -218,6 +229,18 @@ int nsw_weighted_metrics_unnorm(const void* pred, int pred_dtype, const float* t
                                 int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
                                 int64_t Cch, double* rmse, double* acc, void* workspace,
                                 size_t workspace_bytes, void* stream);
+
+/* nsw_weighted_metrics_unnorm with float64 statistics (std_c / mean_c
+ * float64 [Cch]): the reference's torch.as_tensor(stats) keeps the dtype of
+ * the stats file (utils/dataloaders/era5hdf5.py:111-122, utils/inferencer.py
+ * :390-391,405-412), and float64 statistics promote the unnormalised fields,
+ * their difference and its square to float64; here they are computed in
+ * float64 likewise. */
+int nsw_weighted_metrics_unnorm_f64stats(const void* pred, int pred_dtype, const float* target,
+                                         const double* std_c, const double* mean_c, const double* w,
+                                         int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
+                                         int64_t Cch, double* rmse, double* acc, void* workspace,
+                                         size_t workspace_bytes, void* stream);
 
 /* Block.forward's first half with norm1 fused (models/swin_helpers.py:446 +
  * :402-412 + WindowMultiHeadAttention.forward :212-241): qkv[m] (window order,

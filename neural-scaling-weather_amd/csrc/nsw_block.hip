@@ -5,7 +5,7 @@
 //   K3  o   = window attention(qkv) with the shift mask from indices
 //   K4  h1  = scatter_to_tokens(o . Wproj^T + bproj) + x           (MFMA GEMM)
 //   K5  hn  = rmsnorm(h1; norm2)
-//   K6  u   = gelu(hn . W1^T + b1)                                 (MFMA GEMM)
+//   K6  u   = gelu(hn . W1^T + b1)  (erf form, or the tanh form)   (MFMA GEMM)
 //   K7  y   = u . W2^T + b2 + h1                                   (MFMA GEMM)
 //
 // With the norm-folded weight w1_n2 = W1 * norm2 (per input column), K5
@@ -91,6 +91,8 @@ extern "C" int nsw_swin_block_forward(const void* x, void* y, const nsw_block_pa
   const int64_t hd = C / s->num_heads;
   float* S = (float*)(ws + lay.ss);
   const int64_t nparts = sumsq_parts(C, s->dtype);
+  NSW_CHECK_ARG(s->gelu_tanh == 0 || s->gelu_tanh == 1, "%s: gelu_tanh must be 0 or 1", what);
+  const int gelu_epi = s->gelu_tanh ? NSW_EPI_BIAS_GELU_TANH : NSW_EPI_BIAS_GELU;
   int rc;
   if (p->wqkv_n1) {
     // K2'
@@ -116,7 +118,7 @@ extern "C" int nsw_swin_block_forward(const void* x, void* y, const nsw_block_pa
   if (rc) return rc;
   if (p->w1_n2) {
     // K6' (u overwrites qkv in Q)
-    rc = gemm_linear_rowscale(H1, p->w1_n2, p->b1, nullptr, Q, S, nparts, M, s->hidden, C, NSW_EPI_BIAS_GELU,
+    rc = gemm_linear_rowscale(H1, p->w1_n2, p->b1, nullptr, Q, S, nparts, M, s->hidden, C, gelu_epi,
                               s->eps, s->dtype, stream);
     if (rc) return rc;
   } else {
@@ -124,7 +126,7 @@ extern "C" int nsw_swin_block_forward(const void* x, void* y, const nsw_block_pa
     rc = nsw_rmsnorm(H1, p->norm2_w, s->eps, A, M, C, s->dtype, stream);
     if (rc) return rc;
     // K6 (u overwrites qkv in Q)
-    rc = nsw_linear(A, p->w1, p->b1, nullptr, Q, M, s->hidden, C, NSW_EPI_BIAS_GELU, s->dtype, stream);
+    rc = nsw_linear(A, p->w1, p->b1, nullptr, Q, M, s->hidden, C, gelu_epi, s->dtype, stream);
     if (rc) return rc;
   }
   // K7

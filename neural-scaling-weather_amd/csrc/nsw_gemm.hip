@@ -44,6 +44,7 @@ enum Epi {
   EPI_BIAS = NSW_EPI_BIAS,
   EPI_BIAS_GELU = NSW_EPI_BIAS_GELU,
   EPI_BIAS_RESIDUAL = NSW_EPI_BIAS_RESIDUAL,
+  EPI_BIAS_GELU_TANH = NSW_EPI_BIAS_GELU_TANH,
   EPI_SCATTER_RESIDUAL = 11, // bias, row m -> token_of_row(m), + skip[token]
   EPI_QKV_HN16 = 16,         // bias, then per-head RMSNorm of the q and k
   EPI_QKV_HN32 = 32,         // columns, for head dims 16 / 32 / 64
@@ -138,6 +139,17 @@ __device__ __forceinline__ float gelu_erf(float v) {
   h = fmaf(h, t, -0.127414796f);
   h *= t;                                   // -erfc(x) / 2
   return fmaf(h * e, a, fmaxf(v, 0.0f));
+}
+
+// GELU with the tanh form (nn.GELU(approximate="tanh"), the "gelu" of the
+// reference's Transformer-Engine block): 0.5 v (1 + tanh(u)),
+// u = sqrt(2/pi) (v + 0.044715 v^3).  As 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)):
+// GELU(v) = v / (1 + exp2(v (c1 + c3 v^2))) with c1 = -2 sqrt(2/pi) log2(e),
+// c3 = 0.044715 c1.  Saturates cleanly: exp2 -> inf gives 0, exp2 -> 0 gives v.
+__device__ __forceinline__ float gelu_tanh(float v) {
+  const float z = v * v;
+  const float a = v * fmaf(-0.10294324f, z, -2.3022082f);
+  return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a));
 }
 
 template <typename T>
@@ -500,6 +512,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[nb][r] = gelu_erf(v[nb][r]);
+    } else if constexpr (EPI == EPI_BIAS_GELU_TANH) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[nb][r] = gelu_tanh(v[nb][r]);
     }
   };
 
@@ -740,6 +757,8 @@ int gemm_linear_rowscale(const void* x, const void* w_n, const void* bias, const
     case NSW_EPI_BIAS: return dispatch_gemm<EPI_BIAS, PRE_ROWSCALE>(dtype, x, w_n, y, M, N, K, ea, stream, what);
     case NSW_EPI_BIAS_GELU:
       return dispatch_gemm<EPI_BIAS_GELU, PRE_ROWSCALE>(dtype, x, w_n, y, M, N, K, ea, stream, what);
+    case NSW_EPI_BIAS_GELU_TANH:
+      return dispatch_gemm<EPI_BIAS_GELU_TANH, PRE_ROWSCALE>(dtype, x, w_n, y, M, N, K, ea, stream, what);
     case NSW_EPI_BIAS_RESIDUAL:
       NSW_CHECK_ARG(residual != nullptr, "%s: residual epilogue needs a residual", what);
       return dispatch_gemm<EPI_BIAS_RESIDUAL, PRE_ROWSCALE>(dtype, x, w_n, y, M, N, K, ea, stream, what);
@@ -824,6 +843,8 @@ extern "C" int nsw_linear(const void* x, const void* w, const void* bias, const 
     case NSW_EPI_NONE: return dispatch_gemm<EPI_NONE>(dtype, x, w, y, M, N, K, ea, stream, what);
     case NSW_EPI_BIAS: return dispatch_gemm<EPI_BIAS>(dtype, x, w, y, M, N, K, ea, stream, what);
     case NSW_EPI_BIAS_GELU: return dispatch_gemm<EPI_BIAS_GELU>(dtype, x, w, y, M, N, K, ea, stream, what);
+    case NSW_EPI_BIAS_GELU_TANH:
+      return dispatch_gemm<EPI_BIAS_GELU_TANH>(dtype, x, w, y, M, N, K, ea, stream, what);
     case NSW_EPI_BIAS_RESIDUAL:
       NSW_CHECK_ARG(residual != nullptr, "%s: residual epilogue needs a residual", what);
       return dispatch_gemm<EPI_BIAS_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);

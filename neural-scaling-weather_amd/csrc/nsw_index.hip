@@ -267,3 +267,96 @@ extern "C" int nsw_make_attention_mask(float* mask, int64_t H, int64_t W, int64_
                      (hipStream_t)stream, mask, g, total);
   return check_launch("nsw_make_attention_mask");
 }
+
+// ------------------------------------------------------------- LayerNorm ----
+// nn.LayerNorm over the last dim (NormLayer with norm_type="layer_norm",
+// models/layer_helpers.py:94-100,118-119): y = (x - mean) / sqrt(var + eps)
+// * w + b with the biased variance, w / b optional (elementwise_affine).
+// One wave per row, the row held in registers: mean first, then the
+// variance of the centred values (two passes over registers, one over HBM).
+namespace nsw {
+
+template <typename T, int CH>
+__global__ __launch_bounds__(256) void layernorm_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                        const T* __restrict__ b, float eps,
+                                                        T* __restrict__ y, int64_t rows, int C) {
+  constexpr int VEC = Vec16<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= rows) return;
+  const T* xr = x + m * C;
+  T* yr = y + m * C;
+  float v[CH][VEC];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c0 = (lane + 64 * k) * VEC;
+    if (c0 < C) {
+      load16<T>(xr + c0, v[k]);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += v[k][e];
+    }
+  }
+  const float mean = wave_sum(s) / (float)C;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c0 = (lane + 64 * k) * VEC;
+    if (c0 < C) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        v[k][e] -= mean;
+        q += v[k][e] * v[k][e];
+      }
+    }
+  }
+  const float rs = 1.0f / sqrtf(wave_sum(q) / (float)C + eps);
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c0 = (lane + 64 * k) * VEC;
+    if (c0 < C) {
+      float wv[VEC], bv[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) { wv[e] = 1.f; bv[e] = 0.f; }
+      if (w != nullptr) load16<T>(w + c0, wv);
+      if (b != nullptr) load16<T>(b + c0, bv);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[k][e] = (v[k][e] * rs) * wv[e] + bv[e];
+      store16<T>(yr + c0, v[k]);
+    }
+  }
+}
+
+template <typename T>
+static int launch_layernorm(const void* x, const void* w, const void* b, float eps, void* y, int64_t rows,
+                            int64_t C, hipStream_t st) {
+  const char* what = "nsw_layernorm";
+  constexpr int VEC = Vec16<T>::N;
+  NSW_CHECK_ARG(rows >= 0, "%s: rows < 0", what);
+  NSW_CHECK_ARG(C > 0 && C % VEC == 0, "%s: C=%lld must be a positive multiple of %d", what, (long long)C, VEC);
+  NSW_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0 && ((uintptr_t)w % 16) == 0 &&
+                    ((uintptr_t)b % 16) == 0,
+                "%s: pointers must be 16-byte aligned", what);
+  if (rows == 0) return NSW_OK;
+  const int64_t per_lane = (C / VEC + 63) / 64;
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  const T *xp = (const T*)x, *wp = (const T*)w, *bp = (const T*)b;
+  T* yp = (T*)y;
+  if (per_lane <= 1) hipLaunchKernelGGL((layernorm_kernel<T, 1>), grid, block, 0, st, xp, wp, bp, eps, yp, rows, (int)C);
+  else if (per_lane <= 2) hipLaunchKernelGGL((layernorm_kernel<T, 2>), grid, block, 0, st, xp, wp, bp, eps, yp, rows, (int)C);
+  else if (per_lane <= 4) hipLaunchKernelGGL((layernorm_kernel<T, 4>), grid, block, 0, st, xp, wp, bp, eps, yp, rows, (int)C);
+  else if (per_lane <= 8) hipLaunchKernelGGL((layernorm_kernel<T, 8>), grid, block, 0, st, xp, wp, bp, eps, yp, rows, (int)C);
+  else if (per_lane <= 16) hipLaunchKernelGGL((layernorm_kernel<T, 16>), grid, block, 0, st, xp, wp, bp, eps, yp, rows, (int)C);
+  else return set_error(NSW_ERR_UNSUPPORTED, "%s: C=%lld too large (max %d)", what, (long long)C, 64 * 16 * VEC);
+  return check_launch(what);
+}
+
+}  // namespace nsw
+
+extern "C" int nsw_layernorm(const void* x, const void* w, const void* b, float eps, void* y, int64_t rows,
+                             int64_t C, int dtype, void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NSW_DTYPE_BF16) return nsw::launch_layernorm<nsw::bf16>(x, w, b, eps, y, rows, C, st);
+  if (dtype == NSW_DTYPE_F32) return nsw::launch_layernorm<float>(x, w, b, eps, y, rows, C, st);
+  return nsw::set_error(NSW_ERR_INVALID, "nsw_layernorm: unknown dtype %d", dtype);
+}

@@ -22,13 +22,17 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 // AFFINE: both fields are first unnormalised per channel, x * std + mean,
 // rounded after the product and after the sum as the reference's two
 // separate tensor ops do (utils/inferencer.py:390-391,408-409).
-template <typename TP, bool VEC4, bool ACC, bool FULLW, bool AFFINE>
+// TS: dtype of std / mean and of the unnormalised fields.  float64 statistics
+// (torch.as_tensor of float64 .h5 stats, utils/dataloaders/era5hdf5.py:111-122)
+// promote the reference's unnormalised fields, their difference and its
+// square to float64, so the whole per-point chain then runs in TS.
+template <typename TP, typename TS, bool VEC4, bool ACC, bool FULLW, bool AFFINE>
 __global__ __launch_bounds__(256) void wsum_partial_kernel(const TP* __restrict__ pred,
                                                            const float* __restrict__ tgt,
                                                            const double* __restrict__ wlat,
                                                            const float* __restrict__ clim,
-                                                           const float* __restrict__ std_c,
-                                                           const float* __restrict__ mean_c, int H,
+                                                           const TS* __restrict__ std_c,
+                                                           const TS* __restrict__ mean_c, int H,
                                                            int W, int Cch, int rpc, int nchunk,
                                                            double* __restrict__ partial) {
   const int64_t plane = blockIdx.x / nchunk;
@@ -36,21 +40,22 @@ __global__ __launch_bounds__(256) void wsum_partial_kernel(const TP* __restrict_
   const int h0 = ch * rpc;
   const int h1 = min(H, h0 + rpc);
   const int cidx = (int)(plane % Cch);
-  const float cl = ACC ? clim[cidx] : 0.f;
-  const float sc = AFFINE ? std_c[cidx] : 1.f;
-  const float of = AFFINE ? mean_c[cidx] : 0.f;
+  const TS cl = ACC ? (TS)clim[cidx] : (TS)0;
+  const TS sc = AFFINE ? std_c[cidx] : (TS)1;
+  const TS of = AFFINE ? mean_c[cidx] : (TS)0;
   const TP* pp = pred + plane * (int64_t)H * W;
   const float* tp = tgt + plane * (int64_t)H * W;
   double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
-  auto acc1 = [&](float p, float t, double w) {
+  auto acc1 = [&](float pf, float tf, double w) {
+    TS p = (TS)pf, t = (TS)tf;
     if constexpr (AFFINE) {
       // two roundings, never an FMA (the device default contracts a*b+c)
 #pragma clang fp contract(off)
       p = p * sc + of;
       t = t * sc + of;
     }
-    const float d = p - t;
-    const float d2 = d * d;
+    const TS d = p - t;
+    const TS d2 = d * d;
     s0 += w * (double)d2;
     if constexpr (ACC) {
       const double af = (double)(p - cl), ao = (double)(t - cl);
@@ -132,13 +137,13 @@ extern "C" size_t nsw_weighted_metrics_workspace_size(int64_t P, int64_t H, int6
   return (size_t)P * nchunk * 4 * sizeof(double);
 }
 
-template <typename TP, bool FULLW, bool AFFINE>
+template <typename TP, typename TS, bool FULLW, bool AFFINE>
 static void launch_partial(bool vec4, bool acc, dim3 grid, hipStream_t st, const TP* pred,
-                           const float* target, const double* w, const float* clim, const float* sc,
-                           const float* of, int H, int W, int Cch, int rpc, int nchunk, double* partial) {
+                           const float* target, const double* w, const float* clim, const TS* sc,
+                           const TS* of, int H, int W, int Cch, int rpc, int nchunk, double* partial) {
   dim3 block(256);
-#define NSW_PARTIAL(V4, AC)                                                                             \
-  hipLaunchKernelGGL((wsum_partial_kernel<TP, V4, AC, FULLW, AFFINE>), grid, block, 0, st, pred, target, \
+#define NSW_PARTIAL(V4, AC)                                                                                 \
+  hipLaunchKernelGGL((wsum_partial_kernel<TP, TS, V4, AC, FULLW, AFFINE>), grid, block, 0, st, pred, target, \
                      w, clim, sc, of, H, W, Cch, rpc, nchunk, partial)
   if (vec4 && acc) NSW_PARTIAL(true, true);
   else if (vec4) NSW_PARTIAL(true, false);
@@ -147,9 +152,9 @@ static void launch_partial(bool vec4, bool acc, dim3 grid, hipStream_t st, const
 #undef NSW_PARTIAL
 }
 
-template <typename TP, bool AFFINE>
+template <typename TP, typename TS, bool AFFINE>
 static int run_metrics(const TP* pred, const float* target, const double* w, int64_t w_cols,
-                       const float* clim, const float* sc, const float* of, int64_t P, int64_t H,
+                       const float* clim, const TS* sc, const TS* of, int64_t P, int64_t H,
                        int64_t W, int64_t Cch, double* rmse, double* acc, void* workspace,
                        size_t workspace_bytes, hipStream_t st, const char* what) {
   NSW_CHECK_ARG(P > 0 && H > 0 && W > 0 && Cch > 0, "%s: P, H, W, Cch must be positive", what);
@@ -167,10 +172,10 @@ static int run_metrics(const TP* pred, const float* target, const double* w, int
   const bool vec4 = (W % 4 == 0) && ((uintptr_t)pred % (4 * sizeof(TP)) == 0) && ((uintptr_t)target % 16 == 0);
   dim3 grid((unsigned)(P * nchunk));
   if (w_cols == 1 || W == 1)
-    launch_partial<TP, false, AFFINE>(vec4, clim != nullptr, grid, st, pred, target, w, clim, sc, of, (int)H,
+    launch_partial<TP, TS, false, AFFINE>(vec4, clim != nullptr, grid, st, pred, target, w, clim, sc, of, (int)H,
                                       (int)W, (int)Cch, rpc, nchunk, partial);
   else
-    launch_partial<TP, true, AFFINE>(vec4, clim != nullptr, grid, st, pred, target, w, clim, sc, of, (int)H,
+    launch_partial<TP, TS, true, AFFINE>(vec4, clim != nullptr, grid, st, pred, target, w, clim, sc, of, (int)H,
                                      (int)W, (int)Cch, rpc, nchunk, partial);
   int rc = check_launch(what);
   if (rc) return rc;
@@ -183,7 +188,7 @@ extern "C" int nsw_weighted_metrics(const float* pred, const float* target, cons
                                     int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
                                     int64_t Cch, double* rmse, double* acc, void* workspace,
                                     size_t workspace_bytes, void* stream) {
-  return run_metrics<float, false>(pred, target, w, w_cols, clim, nullptr, nullptr, P, H, W, Cch, rmse, acc,
+  return run_metrics<float, float, false>(pred, target, w, w_cols, clim, nullptr, nullptr, P, H, W, Cch, rmse, acc,
                                    workspace, workspace_bytes, (hipStream_t)stream, "nsw_weighted_metrics");
 }
 
@@ -195,10 +200,26 @@ extern "C" int nsw_weighted_metrics_unnorm(const void* pred, int pred_dtype, con
   const char* what = "nsw_weighted_metrics_unnorm";
   hipStream_t st = (hipStream_t)stream;
   if (pred_dtype == NSW_DTYPE_F32)
-    return run_metrics<float, true>((const float*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W, Cch,
-                                    rmse, acc, workspace, workspace_bytes, st, what);
+    return run_metrics<float, float, true>((const float*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W,
+                                           Cch, rmse, acc, workspace, workspace_bytes, st, what);
   if (pred_dtype == NSW_DTYPE_BF16)
-    return run_metrics<bf16, true>((const bf16*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W, Cch,
-                                   rmse, acc, workspace, workspace_bytes, st, what);
+    return run_metrics<bf16, float, true>((const bf16*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W,
+                                          Cch, rmse, acc, workspace, workspace_bytes, st, what);
+  return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, pred_dtype);
+}
+
+extern "C" int nsw_weighted_metrics_unnorm_f64stats(const void* pred, int pred_dtype, const float* target,
+                                                    const double* std_c, const double* mean_c, const double* w,
+                                                    int64_t w_cols, const float* clim, int64_t P, int64_t H,
+                                                    int64_t W, int64_t Cch, double* rmse, double* acc,
+                                                    void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "nsw_weighted_metrics_unnorm_f64stats";
+  hipStream_t st = (hipStream_t)stream;
+  if (pred_dtype == NSW_DTYPE_F32)
+    return run_metrics<float, double, true>((const float*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W,
+                                            Cch, rmse, acc, workspace, workspace_bytes, st, what);
+  if (pred_dtype == NSW_DTYPE_BF16)
+    return run_metrics<bf16, double, true>((const bf16*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W,
+                                           Cch, rmse, acc, workspace, workspace_bytes, st, what);
   return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, pred_dtype);
 }

@@ -23,6 +23,7 @@ NSW_EPI_NONE = 0
 NSW_EPI_BIAS = 1
 NSW_EPI_BIAS_GELU = 2
 NSW_EPI_BIAS_RESIDUAL = 3
+NSW_EPI_BIAS_GELU_TANH = 4
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -39,7 +40,7 @@ class BlockParams(ctypes.Structure):
 class BlockShape(ctypes.Structure):
     _fields_ = [("B", _i64), ("T", _i64), ("H", _i64), ("W", _i64), ("C", _i64),
                 ("num_heads", _i64), ("ws0", _i64), ("ws1", _i64), ("s0", _i64), ("s1", _i64),
-                ("hidden", _i64), ("eps", _f32), ("dtype", _int)]
+                ("hidden", _i64), ("eps", _f32), ("dtype", _int), ("gelu_tanh", _int)]
 
 
 # name -> (restype, argtypes); must match include/nsw.h
@@ -56,6 +57,7 @@ SIGNATURES = {
     "nsw_make_attention_mask": (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "nsw_selftest_fastdiv": (_int, []),
     "nsw_rmsnorm": (_int, [_vp, _vp, _f32, _vp, _i64, _i64, _int, _vp]),
+    "nsw_layernorm": (_int, [_vp, _vp, _vp, _f32, _vp, _i64, _i64, _int, _vp]),
     "nsw_rmsnorm_roll_partition": (_int, [_vp, _vp, _f32, _vp, _i64, _i64, _i64, _i64, _i64,
                                           _i64, _i64, _i64, _i64, _int, _vp]),
     "nsw_linear": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _vp]),
@@ -72,6 +74,8 @@ SIGNATURES = {
                                     ctypes.c_size_t, _vp]),
     "nsw_weighted_metrics_unnorm": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
                                            _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "nsw_weighted_metrics_unnorm_f64stats": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
+                                                    _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "nsw_qkv_projection_norm_gather": (_int, [_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _i64, _i64, _i64, _i64,
                                               _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "nsw_linear_rownorm": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _f32, _int, _vp]),

@@ -16,6 +16,13 @@ vanilla <-> TE correspondence is the one the reference's own test spells out
     mlp.fc2.weight / mlp.bias2.bias      rms_norm_mlp.fc2_weight / fc2_bias
 
 TE's ``*_extra_state`` entries carry FP8 metadata and are dropped.
+
+The TE block also computes differently from the vanilla one: its norms are
+te.RMSNorm / te.LayerNormMLP at their default eps = 1e-5 (the vanilla
+nn.RMSNorm(eps=None) takes finfo(dtype).eps) and its MLP activation "gelu" is
+the tanh form (the vanilla block uses the exact erf).  ``apply_te_semantics``
+switches a model's blocks to that arithmetic; ``load_model_checkpoint`` does
+it whenever the file holds TE-layout weights.
 """
 from __future__ import annotations
 
@@ -111,3 +118,44 @@ def load_checkpoint_model_state(path: str) -> "OrderedDict[str, object]":
     import torch
     ck = torch.load(path, map_location="cpu", weights_only=True)
     return to_vanilla(ck["model_state"] if "model_state" in ck else ck)
+
+
+TE_EPS = 1e-5
+
+
+def apply_te_semantics(model) -> int:
+    """Give every nsw.Block of ``model`` the TE block's arithmetic: eps = 1e-5
+    on norm1, norm2, q_norm and k_norm (te.RMSNorm / te.LayerNormMLP defaults,
+    models/swin_helpers_te.py:132-137, 302, 318) and the tanh-form GELU (TE's
+    "gelu", :318-323).  Returns the number of blocks changed."""
+    from torch import nn
+
+    from .swin_helpers import Block
+    n = 0
+    for m in model.modules():
+        if isinstance(m, Block):
+            for norm in (m.norm1, m.norm2, m.attn.q_norm, m.attn.k_norm):
+                norm.norm.eps = TE_EPS
+            m.mlp.act = nn.GELU(approximate="tanh")
+            n += 1
+    return n
+
+
+def load_model_checkpoint(model, path: str, strict: bool = True, te_semantics: bool = True):
+    """Load a reference checkpoint file (any prefix / TE or vanilla layout)
+    into ``model`` with the safe loader.  When the file holds TE-layout block
+    weights and ``te_semantics`` is set, the blocks are switched to the TE
+    arithmetic (``apply_te_semantics``) so that they compute what the
+    checkpoint was trained with.  Returns (missing, unexpected, te_layout)."""
+    import torch
+    ck = torch.load(path, map_location="cpu", weights_only=True)
+    raw = ck["model_state"] if "model_state" in ck else ck
+    te = is_te_layout(strip_prefixes(raw))
+    sd = to_vanilla(raw)
+    missing, unexpected = model.load_state_dict(sd, strict=False)
+    missing = [k for k in missing if not k.endswith("attn_mask")]
+    if strict and (missing or unexpected):
+        raise RuntimeError(f"checkpoint does not match the model: missing {missing}, unexpected {unexpected}")
+    if te and te_semantics:
+        apply_te_semantics(model)
+    return missing, unexpected, te

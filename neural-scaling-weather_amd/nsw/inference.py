@@ -40,8 +40,13 @@ class Rollout:
                  invariants: Optional[torch.Tensor] = None, clim: Optional[torch.Tensor] = None):
         self.model = model
         dev = model.head.weight.device
-        self.mean = mean.reshape(-1).to(device=dev, dtype=torch.float32)
-        self.std = std.reshape(-1).to(device=dev, dtype=torch.float32)
+        # the statistics keep their dtype: float64 stats make the reference's
+        # unnormalised fields float64 (torch.as_tensor of the stats file,
+        # utils/dataloaders/era5hdf5.py:111-122), fp32 stats keep them fp32
+        mean, std = torch.as_tensor(mean), torch.as_tensor(std)
+        sdt = torch.float64 if torch.float64 in (mean.dtype, std.dtype) else torch.float32
+        self.mean = mean.reshape(-1).to(device=dev, dtype=sdt)
+        self.std = std.reshape(-1).to(device=dev, dtype=sdt)
         self.weights = area_weights.to(device=dev, dtype=torch.float64)
         self.invariants = None if invariants is None else invariants.to(device=dev, dtype=torch.float32).contiguous()
         self.clim = None if clim is None else clim.reshape(-1).to(device=dev, dtype=torch.float32)

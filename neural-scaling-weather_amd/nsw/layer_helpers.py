@@ -61,9 +61,9 @@ class BiasLayer(nn.Module):
 
 
 class NormLayer(nn.Module):
-    """``NormLayer`` (models/layer_helpers.py:75-119).  ``rms_norm`` runs the
-    libnsw RMSNorm kernel; ``layer_norm`` (not on the Swin block path) is
-    constructible for state-dict compatibility but its forward raises."""
+    """``NormLayer`` (models/layer_helpers.py:75-119): ``rms_norm`` runs the
+    libnsw RMSNorm kernel, ``layer_norm`` the libnsw LayerNorm kernel (same
+    parameters and eps as the wrapped nn.RMSNorm / nn.LayerNorm)."""
 
     def __init__(self, normalized_shape, elementwise_affine=True, norm_type="layer_norm",
                  comm_metadata=None):
@@ -82,8 +82,11 @@ class NormLayer(nn.Module):
                 self.norm.bias.comm_metadata = meta
 
     def forward(self, x):
-        if self.norm_type != "rms_norm":
-            raise NotImplementedError("libnsw implements the RMSNorm used by the Swin block only")
+        if self.norm_type == "layer_norm":
+            n = self.norm
+            if len(n.normalized_shape) != 1:
+                raise NotImplementedError("libnsw normalises over the last dim only")
+            return ops.layer_norm(x.contiguous(), n.weight, n.bias, n.eps)
         w = self.norm.weight
         if w is None:
             w = torch.ones(x.shape[-1], dtype=x.dtype, device=x.device)

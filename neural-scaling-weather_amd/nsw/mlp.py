@@ -1,8 +1,11 @@
-"""``MLP`` (models/mlp.py:14-95): fc1 -> +bias1 -> GELU(erf) -> fc2 -> +bias2.
+"""``MLP`` (models/mlp.py:14-95): fc1 -> +bias1 -> GELU -> fc2 -> +bias2.
 
-Two libnsw GEMM launches: fc1 with the bias + exact-erf GELU epilogue, fc2
-with the bias epilogue.  Dropout is the identity in eval (p = 0 in every
-config); a training-mode dropout with p > 0 is not implemented and raises.
+Two libnsw GEMM launches: fc1 with the bias + GELU epilogue, fc2 with the
+bias epilogue.  The GELU is ``act_layer``'s: nn.GELU() (exact erf, the
+reference's default) or nn.GELU(approximate="tanh") (the form of the
+reference's Transformer-Engine block, models/swin_helpers_te.py:318-323).
+Dropout is the identity in eval (p = 0 in every config); a training-mode
+dropout with p > 0 is not implemented and raises.
 """
 from __future__ import annotations
 
@@ -30,10 +33,18 @@ class MLP(nn.Module):
         self.drop = nn.Dropout(drop)
 
     def _check_fusable(self):
-        if not (isinstance(self.act, nn.GELU) and self.act.approximate == "none"):
-            raise NotImplementedError("libnsw fuses the exact-erf nn.GELU only")
+        if not (isinstance(self.act, nn.GELU) and self.act.approximate in ("none", "tanh")):
+            raise NotImplementedError("libnsw fuses nn.GELU (approximate 'none' or 'tanh') only")
         if self.training and self.drop.p > 0:
             raise NotImplementedError("dropout with p > 0 in training mode is not implemented")
+
+    @property
+    def gelu_tanh(self) -> bool:
+        return self.act.approximate == "tanh"
+
+    @property
+    def gelu_epilogue(self) -> int:
+        return _lib.NSW_EPI_BIAS_GELU_TANH if self.gelu_tanh else _lib.NSW_EPI_BIAS_GELU
 
     def forward(self, x, residual=None):
         """``residual`` (same shape as the output) is added in fc2's epilogue;
@@ -41,7 +52,7 @@ class MLP(nn.Module):
         (models/swin_helpers.py:456)."""
         self._check_fusable()
         x = x.contiguous()
-        h = ops.linear(x, self.fc1.weight, self.bias1.bias, epilogue=_lib.NSW_EPI_BIAS_GELU)
+        h = ops.linear(x, self.fc1.weight, self.bias1.bias, epilogue=self.gelu_epilogue)
         if residual is None:
             return ops.linear(h, self.fc2.weight, self.bias2.bias, epilogue=_lib.NSW_EPI_BIAS)
         return ops.linear(h, self.fc2.weight, self.bias2.bias, residual=residual.contiguous(),

@@ -152,6 +152,22 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: Optional[float] = None)
     return y
 
 
+def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],
+               eps: float = 1e-5) -> torch.Tensor:
+    """nn.LayerNorm over the last dim (biased variance); weight / bias may be
+    None (elementwise_affine=False)."""
+    dev = _dev(x, weight, bias)
+    _same_dtype(x, weight, bias)
+    C = x.shape[-1]
+    for t in (weight, bias):
+        if t is not None and t.numel() != C:
+            raise ValueError(f"layer-norm parameter has {t.numel()} elements, input has {C} features")
+    y = torch.empty_like(x)
+    check(lib().nsw_layernorm(x.data_ptr(), _p(weight), _p(bias), float(eps), y.data_ptr(), x.numel() // C, C,
+                              dtype_code(x), _stream(dev)), "layer_norm")
+    return y
+
+
 def rmsnorm_roll_partition(x: torch.Tensor, weight: torch.Tensor, window_size, shift_size,
                            eps: Optional[float] = None) -> torch.Tensor:
     """norm1 + roll by -shift + window_partition, as [B*nW, T*wa, C]."""
@@ -258,14 +274,20 @@ def linear_rownorm(x: torch.Tensor, w_n: torch.Tensor, bias: Optional[torch.Tens
 def window_attention(qkv: torch.Tensor, num_heads: int, scale: float, mask: Optional[torch.Tensor] = None,
                      geometry: Optional[Tuple[int, int, Tuple[int, int], Tuple[int, int], int]] = None
                      ) -> torch.Tensor:
-    """qkv [Bw, L, 3C] -> o [Bw, L, C].  ``mask``: additive fp32 [nW, L, L] or
-    None; ``geometry`` = (H, W, window_size, shift_size, T) computes the
-    reference's shift mask from indices instead (ignored when mask is given)."""
+    """qkv [Bw, L, 3C] -> o [Bw, L, C].  ``mask`` [nW, L, L] or None, with
+    F.scaled_dot_product_attention's meaning (models/swin_helpers.py:247): a
+    float mask is added to the scaled logits, a boolean mask marks the keys
+    that take part (True) and is applied as 0 / -inf.  ``geometry`` = (H, W,
+    window_size, shift_size, T) computes the reference's shift mask from
+    indices instead (ignored when mask is given)."""
     Bw, L, C3 = qkv.shape
     C = C3 // 3
     dev = _dev(qkv, mask)
     if mask is not None:
-        if mask.dtype != torch.float32:
+        if mask.dtype == torch.bool:
+            mask = torch.zeros(mask.shape, dtype=torch.float32, device=mask.device).masked_fill_(
+                ~mask, float("-inf"))
+        elif mask.dtype != torch.float32:
             mask = mask.float().contiguous()
         if mask.shape[-2:] != (L, L):
             raise ValueError(f"mask shape {tuple(mask.shape)} does not match L={L}")
@@ -362,21 +384,24 @@ def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 
 
 def block_shape(x: torch.Tensor, num_heads: int, window_size, shift_size, hidden: int,
-                eps: Optional[float]) -> _lib.BlockShape:
+                eps: Optional[float], gelu_tanh: bool = False) -> _lib.BlockShape:
     B, T, H, W, C = x.shape
     eps = default_eps(x.dtype) if eps is None else float(eps)
     return _lib.BlockShape(B, T, H, W, C, num_heads, window_size[0], window_size[1],
-                           int(shift_size[0]), int(shift_size[1]), hidden, eps, dtype_code(x))
+                           int(shift_size[0]), int(shift_size[1]), hidden, eps, dtype_code(x),
+                           1 if gelu_tanh else 0)
 
 
 def swin_block_forward(x: torch.Tensor, packed: dict, num_heads: int, window_size, shift_size,
-                       eps: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       eps: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                       gelu_tanh: bool = False) -> torch.Tensor:
     """Whole Block.forward through one C-ABI call.  ``packed`` holds the
-    tensors named like the fields of nsw_block_params."""
+    tensors named like the fields of nsw_block_params; ``gelu_tanh`` selects
+    the tanh-form GELU (the reference's TE block) instead of the erf form."""
     dev = _dev(x, *packed.values())
     _same_dtype(x, *packed.values())
     hidden = packed["w1"].shape[0]
-    shp = block_shape(x, num_heads, window_size, shift_size, hidden, eps)
+    shp = block_shape(x, num_heads, window_size, shift_size, hidden, eps, gelu_tanh)
     params = _lib.BlockParams(*[_p(packed.get(n)) for n, _ in _lib.BlockParams._fields_])
     nbytes = lib().nsw_block_workspace_size(shp)
     ws = workspace(nbytes, dev)
@@ -481,7 +506,9 @@ def weighted_metrics_unnorm(pred: torch.Tensor, target: torch.Tensor, std: torch
                             weights: torch.Tensor, clim: Optional[torch.Tensor] = None):
     """Weighted RMSE (and ACC with ``clim``) of pred * std + mean against
     target * std + mean, per (b, t, c), float64 [B, T, C].  pred fp32 or
-    bf16, target fp32, std / mean per channel."""
+    bf16, target fp32, std / mean per channel; float64 std or mean (stats
+    read from a float64 file) make the unnormalised fields float64, as the
+    reference's type promotion does, otherwise they are fp32."""
     if pred.shape != target.shape or pred.dim() != 5:
         raise ValueError("pred and target must be [B, T, C, H, W] of the same shape")
     if target.dtype != torch.float32:
@@ -495,8 +522,10 @@ def weighted_metrics_unnorm(pred: torch.Tensor, target: torch.Tensor, std: torch
         w_cols = W
     else:
         raise ValueError(f"weights of shape {tuple(weights.shape)} do not match a {H}x{W} field")
-    sc = std.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
-    of = mean.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+    f64 = torch.float64 in (torch.as_tensor(std).dtype, torch.as_tensor(mean).dtype)
+    sdt = torch.float64 if f64 else torch.float32
+    sc = torch.as_tensor(std).reshape(-1).to(device=dev, dtype=sdt).contiguous()
+    of = torch.as_tensor(mean).reshape(-1).to(device=dev, dtype=sdt).contiguous()
     if sc.numel() != C or of.numel() != C:
         raise ValueError("std and mean must have one value per channel")
     if clim is not None:
@@ -508,9 +537,9 @@ def weighted_metrics_unnorm(pred: torch.Tensor, target: torch.Tensor, std: torch
     acc = torch.empty(P, dtype=torch.float64, device=dev) if clim is not None else None
     nbytes = lib().nsw_weighted_metrics_workspace_size(P, H, W)
     ws = workspace(max(nbytes, 8), dev)
-    check(lib().nsw_weighted_metrics_unnorm(pred.data_ptr(), dtype_code(pred), target.data_ptr(), sc.data_ptr(),
-                                            of.data_ptr(), w.data_ptr(), w_cols, _p(clim), P, H, W, C,
-                                            rmse.data_ptr(), _p(acc), ws.data_ptr(), ws.numel(), _stream(dev)),
+    fn = lib().nsw_weighted_metrics_unnorm_f64stats if f64 else lib().nsw_weighted_metrics_unnorm
+    check(fn(pred.data_ptr(), dtype_code(pred), target.data_ptr(), sc.data_ptr(), of.data_ptr(), w.data_ptr(),
+             w_cols, _p(clim), P, H, W, C, rmse.data_ptr(), _p(acc), ws.data_ptr(), ws.numel(), _stream(dev)),
           "weighted_metrics_unnorm")
     rmse = rmse.view(B, T, C)
     return rmse, (acc.view(B, T, C) if acc is not None else None)

@@ -34,8 +34,11 @@ _EMBED_META = {"sharded": [], "shared": ["tp-sp1-sp2"], "reduce": ["sp1-sp2"]}
 
 class Conv2DLayer(nn.Module):
     """``Conv2DLayer`` (models/layer_helpers.py:152-172): holds ``conv`` (an
-    nn.Conv2d, for the parameter names and init); stride = kernel_size is the
-    only case the model uses and the only one the forward runs."""
+    nn.Conv2d, for the parameter names and init).  The forward runs the
+    non-overlapping case the model uses (stride = kernel size, no padding,
+    dilation or groups) as a patch-matrix GEMM: ``nsw_patch_im2col`` then
+    ``nsw_linear`` with the conv bias in the epilogue.  Other convolutions
+    are not on the Swin path and raise."""
 
     def __init__(self, in_chans, out_chans, kernel_size, stride=1, bias=True, comm_metadata=None):
         super().__init__()
@@ -44,9 +47,63 @@ class Conv2DLayer(nn.Module):
         self.conv.weight.comm_metadata = meta
         if bias:
             self.conv.bias.comm_metadata = meta
+        self._pack_key = None
+        self._pack = None
+
+    @property
+    def patch(self) -> int:
+        c = self.conv
+        k, st = tuple(c.kernel_size), tuple(c.stride)
+        if (k[0] != k[1] or st != k or tuple(c.padding) != (0, 0) or tuple(c.dilation) != (1, 1)
+                or c.groups != 1 or c.padding_mode != "zeros"):
+            raise NotImplementedError("libnsw runs the non-overlapping patch convolution (stride = square "
+                                      f"kernel, no padding / dilation / groups); got kernel {k}, stride {st}")
+        return k[0]
+
+    def packed(self):
+        """Weight as a [E, Kp] GEMM operand (rows of the Conv2d weight in
+        (c, u, v) order, zero columns up to the GEMM k granularity), cached
+        until the parameters change."""
+        w, b = self.conv.weight, self.conv.bias
+        key = (w.data_ptr(), w._version, w.dtype, w.device,
+               None if b is None else (b.data_ptr(), b._version))
+        if self._pack_key != key:
+            E = w.shape[0]
+            K = w[0].numel()
+            g = ops.k_granule(w.dtype)
+            Kp = (K + g - 1) // g * g
+            wp = torch.zeros(E, Kp, dtype=w.dtype, device=w.device)
+            with torch.no_grad():
+                wp[:, :K].copy_(w.detach().reshape(E, K))
+            self._pack = (wp, None if b is None else b.detach().contiguous(), Kp)
+            self._pack_key = key
+        return self._pack
+
+    def tokens(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
+               invariants: Optional[torch.Tensor] = None, frame0: int = 0) -> torch.Tensor:
+        """[B, T, C, H, W] (p | H, p | W) -> conv output in token layout
+        [B, T, H/p, W/p, E], plus ``residual`` [B*T*(H/p)*(W/p), E] if given."""
+        B, T, C, H, W = x.shape
+        p = self.patch
+        wp, b, Kp = self.packed()
+        pm = ops.patch_im2col(x.contiguous(), p, Kp, wp.dtype, invariants=invariants, frame0=frame0)
+        if b is None:
+            if residual is not None:
+                raise NotImplementedError("a residual without a conv bias is not fused")
+            y = ops.linear(pm, wp)
+        else:
+            y = ops.linear(pm, wp, b, residual=residual)
+        return y.view(B, T, H // p, W // p, wp.shape[0])
 
     def forward(self, x):
-        raise NotImplementedError("Conv2DLayer runs inside PatchEmbedLayer (stride = kernel size) only")
+        """Conv2d semantics: [N, C, H, W] -> [N, E, H // p, W // p] (rows and
+        columns beyond the last whole patch are ignored, as Conv2d does)."""
+        p = self.patch
+        N, C, H, W = x.shape
+        h, w = H // p, W // p
+        if (H, W) != (h * p, w * p):
+            x = x[:, :, :h * p, :w * p]
+        return self.tokens(x.unsqueeze(1))[:, 0].permute(0, 3, 1, 2).contiguous()
 
 
 class PatchEmbedLayer(nn.Module):
@@ -70,27 +127,9 @@ class PatchEmbedLayer(nn.Module):
         self.sp2_patch_shapes = [s // patch_size for s in sp2_shapes]
         self.w = self.sp2_patch_shapes[0]
         self.num_patches = self.h * self.w
-        self._pack_key = None
-        self._pack = None
 
     def packed(self):
-        """Weight as a [E, Kp] GEMM operand (rows of the Conv2d weight in
-        (c, u, v) order, zero columns up to the GEMM k granularity), cached
-        until the parameters change."""
-        w, b = self.proj.conv.weight, self.proj.conv.bias
-        key = (w.data_ptr(), w._version, w.dtype, w.device,
-               None if b is None else (b.data_ptr(), b._version))
-        if self._pack_key != key:
-            E = w.shape[0]
-            K = w[0].numel()
-            g = ops.k_granule(w.dtype)
-            Kp = (K + g - 1) // g * g
-            wp = torch.zeros(E, Kp, dtype=w.dtype, device=w.device)
-            with torch.no_grad():
-                wp[:, :K].copy_(w.detach().reshape(E, K))
-            self._pack = (wp, None if b is None else b.detach().contiguous(), Kp)
-            self._pack_key = key
-        return self._pack
+        return self.proj.packed()
 
     def tokens(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
                invariants: Optional[torch.Tensor] = None, frame0: int = 0) -> torch.Tensor:
@@ -100,19 +139,11 @@ class PatchEmbedLayer(nn.Module):
         p = self.patch_size
         if H != self.h * p or W != self.w * p:
             raise ValueError(f"input extent {(H, W)} does not match the layer's {(self.h * p, self.w * p)}")
-        wp, b, Kp = self.packed()
-        pm = ops.patch_im2col(x.contiguous(), p, Kp, wp.dtype, invariants=invariants, frame0=frame0)
-        if b is None:
-            if residual is not None:
-                raise NotImplementedError("a residual without a conv bias is not fused")
-            y = ops.linear(pm, wp)
-        else:
-            y = ops.linear(pm, wp, b, residual=residual)
-        return y.view(B, T, H // p, W // p, self.embed_dim)
+        return self.proj.tokens(x, residual=residual, invariants=invariants, frame0=frame0)
 
     def forward(self, x):
         """Conv2d semantics: [N, C, H, W] -> [N, E, H/p, W/p]."""
-        return self.tokens(x.unsqueeze(1))[:, 0].permute(0, 3, 1, 2)
+        return self.proj(x)
 
 
 class SwinTransformer(nn.Module):

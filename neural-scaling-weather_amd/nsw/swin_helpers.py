@@ -46,6 +46,31 @@ def roll_forward_reverseroll_backward(x, shifts, dims, comm_names=None):
     return ops.roll_hw(x.contiguous(), tuple(shifts))
 
 
+def attention_mask_closed_form(H: int, W: int, window_size: Tuple[int, int], shift_size: Tuple[int, int],
+                               T: int = 1) -> torch.Tensor:
+    """``Block._make_attention_mask`` (models/swin_helpers.py:322-397, one GPU,
+    causal=False) on the host: the additive fp32 mask [nW, T*wa, T*wa].
+
+    With a shift, the reference labels the image rows with the slices
+    ``[0:-ws0] = 0`` then ``[-s0:] = 1`` (:353-356) and blocks (-100) the
+    query/key pairs of a window whose rows carry different labels (:371-378);
+    the temporal part is 0 and a token's label does not depend on its frame.
+    Without a shift the mask is 0."""
+    a, b = window_size
+    wa = a * b
+    nhb, nwb = H // a, W // b
+    L = T * wa
+    if not any(shift_size):
+        return torch.zeros(nhb * nwb, L, L)
+    rows = torch.zeros(H)
+    rows[0:H - a] = 0.0
+    rows[-int(shift_size[0]):] = 1.0
+    band = torch.arange(nhb * nwb) // nwb                          # window -> band i
+    r = (torch.arange(L) % wa) // b                                # token -> row in the window
+    lab = rows[band[:, None] * a + r[None, :]]                     # [nW, L]
+    return torch.where(lab[:, :, None] != lab[:, None, :], torch.tensor(-100.0), torch.tensor(0.0))
+
+
 def _eps_of(norm: NormLayer, dtype: torch.dtype) -> float:
     e = norm.norm.eps
     return float(torch.finfo(dtype).eps) if e is None else float(e)
@@ -145,7 +170,11 @@ class Block(nn.Module):
         H, W = self.feat_size
         if H % self.window_size[0] or W % self.window_size[1]:
             raise ValueError(f"feat_size {self.feat_size} is not divisible by window {self.window_size}")
-        self._mask_cache = {}
+        # the reference registers the additive mask as a non-persistent buffer
+        # at construction (models/swin_helpers.py:320,397); Block.forward never
+        # reads it (the attention kernel evaluates the same closed form)
+        self.register_buffer("attn_mask", attention_mask_closed_form(
+            H, W, self.window_size, self.shift_size, temporal_context_window_size), persistent=False)
         self._pack_key = None
         self._pack = None
         # fold_norm2: the proj GEMM writes the row sums of squares of h1 and
@@ -158,26 +187,9 @@ class Block(nn.Module):
         self.fold_norm1 = False
         self.fold_norm2 = True
 
-    # The reference registers attn_mask [nW, T*wa, T*wa] as a non-persistent
-    # buffer (models/swin_helpers.py:397).  Here it is materialised on demand
-    # on the GPU by the mask kernel; Block.forward never reads it (the
-    # attention kernel evaluates the same closed form from indices).
     def attention_mask(self, device) -> torch.Tensor:
-        device = torch.device(device)
-        m = self._mask_cache.get(device)
-        if m is None:
-            H, W = self.feat_size
-            m = ops.make_attention_mask(H, W, self.window_size, self.shift_size,
-                                        self.temporal_context_window_size, device)
-            self._mask_cache[device] = m
-        return m
-
-    @property
-    def attn_mask(self) -> torch.Tensor:
-        dev = self.norm1.norm.weight.device
-        if dev.type != "cuda":
-            raise RuntimeError("attn_mask is built by a HIP kernel; move the block to the GPU first")
-        return self.attention_mask(dev)
+        """The additive mask on ``device`` as fp32 (the buffer's values)."""
+        return self.attn_mask.to(device=device, dtype=torch.float32)
 
     def _eps(self, dtype) -> float:
         es = {_eps_of(n, dtype) for n in (self.norm1, self.norm2, self.attn.q_norm, self.attn.k_norm)}
@@ -236,7 +248,7 @@ class Block(nn.Module):
         if drop:
             pk = {k: v for k, v in pk.items() if k not in drop}
         return ops.swin_block_forward(x.contiguous(), pk, self.num_heads, self.window_size,
-                                      self.shift_size, eps=self._eps(x.dtype))
+                                      self.shift_size, eps=self._eps(x.dtype), gelu_tanh=self.mlp.gelu_tanh)
 
 
 # Names used by north_star / other Swin code bases.

@@ -53,8 +53,25 @@ def model_coords(spatial: torch.Tensor, T: int) -> torch.Tensor:
 
 def patch_conv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], p: int) -> torch.Tensor:
     """``PatchEmbedLayer.forward`` = ``Conv2d(k=p, stride=p)``
-    (models/layer_helpers.py:138-172): [N, C, H, W] -> [N, E, H/p, W/p]."""
-    return F.conv2d(x, weight, bias, stride=p)
+    (models/layer_helpers.py:138-172): [N, C, H, W] -> [N, E, H/p, W/p].
+    On a GPU device the same convolution is evaluated by
+    :func:`patch_conv_unfold` (no run-time convolution kernel compilation)."""
+    if x.device.type == "cpu":
+        return F.conv2d(x, weight, bias, stride=p)
+    return patch_conv_unfold(x, weight, bias, p)
+
+
+def patch_conv_unfold(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], p: int) -> torch.Tensor:
+    """The stride-p convolution as ``F.unfold`` (the patch matrix, columns in
+    the (c, u, v) order of the flattened Conv2d weight) times the weight
+    (tests check it against ``F.conv2d`` and a brute-force im2col)."""
+    N, C, H, W = x.shape
+    E = weight.shape[0]
+    cols = F.unfold(x, kernel_size=p, stride=p)                     # [N, C*p*p, h*w]
+    y = torch.matmul(weight.reshape(E, -1), cols)                   # [N, E, h*w]
+    if bias is not None:
+        y = y + bias.view(1, E, 1)
+    return y.view(N, E, H // p, W // p)
 
 
 def prepare_tokens(x: torch.Tensor, pe_w: torch.Tensor, pe_b: torch.Tensor, p: int,
@@ -95,7 +112,8 @@ def block_shift(i: int, window_size: Tuple[int, int]) -> Tuple[int, int]:
 
 def model_forward(x: torch.Tensor, params: Dict[str, torch.Tensor], *, patch_size: int,
                   window_size: Tuple[int, int], depth: int, num_heads: int, out_chans: int,
-                  coords: Optional[torch.Tensor] = None, eps: Optional[float] = None) -> torch.Tensor:
+                  coords: Optional[torch.Tensor] = None, eps: Optional[float] = None,
+                  gelu: str = "none") -> torch.Tensor:
     """``SwinTransformer.forward`` (models/swin.py:301-323) without the big
     skip convolution (``use_big_skip_conv=False``, the default).  ``params``
     uses the reference's state-dict names; ``coords`` is [T, H, W, 4] for the
@@ -111,7 +129,8 @@ def model_forward(x: torch.Tensor, params: Dict[str, torch.Tensor], *, patch_siz
     y = prepare_tokens(x, params["patch_embed.proj.conv.weight"], params["patch_embed.proj.conv.bias"], p, pos)
     for i in range(depth):
         bp = {k[len(f"blocks.{i}."):]: v for k, v in params.items() if k.startswith(f"blocks.{i}.")}
-        y = swin_ref.block_forward(y, bp, num_heads, window_size, block_shift(i, window_size), eps=eps)
+        y = swin_ref.block_forward(y, bp, num_heads, window_size, block_shift(i, window_size), eps=eps,
+                                   gelu=gelu)
     y = forward_head(y, params["head.weight"], p, out_chans)
     return y[:, -1:]
 
@@ -149,19 +168,21 @@ def rollout(model, input_window: torch.Tensor, invariants: Optional[torch.Tensor
     win = input_window.clone()
     S = targets.shape[0]
     rm, ac, gens = [], [], []
-    ms, ss = mean.view(1, 1, -1, 1, 1), std.view(1, 1, -1, 1, 1)
+    dev = input_window.device
+    ms, ss = mean.view(1, 1, -1, 1, 1).to(dev), std.view(1, 1, -1, 1, 1).to(dev)
     for i in range(S):
         inp = win
         if invariants is not None:
             B, T, _, H, W = win.shape
-            inp = torch.cat([win, invariants.view(1, 1, -1, H, W).expand(B, T, -1, H, W)], dim=2)
+            inv = invariants.to(dev).view(1, 1, -1, H, W).expand(B, T, -1, H, W)
+            inp = torch.cat([win, inv], dim=2)
         gen = model(inp)
         pred = gen.float() * ss + ms
-        targ = targets[i].view(1, 1, *targets.shape[1:]).float() * ss + ms
-        pn, tn = pred.double().numpy(), targ.double().numpy()
+        targ = targets[i].view(1, 1, *targets.shape[1:]).to(dev).float() * ss + ms
+        pn, tn = pred.double().cpu().numpy(), targ.double().cpu().numpy()
         rm.append(metrics_ref.weighted_rmse(pn, tn, np.asarray(w_lat)))
         if clim is not None:
-            ac.append(metrics_ref.weighted_acc(pn, tn, np.asarray(w_lat), clim.double().numpy()))
+            ac.append(metrics_ref.weighted_acc(pn, tn, np.asarray(w_lat), clim.double().cpu().numpy()))
         gens.append(gen[0, 0].float())
         win = torch.roll(win, shifts=-1, dims=1)
         win[:, -1] = gen[:, 0].to(win.dtype)

@@ -3,7 +3,9 @@
 Every function follows one reference routine, cited by file:line of
 ShashankSubramanian/neural-scaling-weather.  The op sequence (including where
 the residuals, norms, biases and the additive mask enter) is the reference's;
-the code is an independent eager-mode restatement in plain PyTorch on the CPU.
+the code is an independent eager-mode restatement in plain PyTorch, run on
+the CPU, or (for the full-size checks) with fp32 library kernels on a GPU
+device, whichever device its inputs are on.
 
 Single-GPU semantics: every communicator has size 1, so the reference's
 distributed wrappers (``identity_forward_allreduce_backward``,
@@ -71,7 +73,7 @@ def window_reverse(windows: torch.Tensor, window_size: Tuple[int, int],
 
 def make_attention_mask(H: int, W: int, window_size: Tuple[int, int],
                         shift_size: Tuple[int, int], T: int = 1,
-                        causal: bool = False) -> torch.Tensor:
+                        causal: bool = False, device=None) -> torch.Tensor:
     """``Block._make_attention_mask`` (models/swin_helpers.py:322-397), one GPU
     (sp shapes [H], [W]).  Returns the additive fp32 mask [nW, T*wa, T*wa].
 
@@ -100,7 +102,8 @@ def make_attention_mask(H: int, W: int, window_size: Tuple[int, int],
         nW = (H // a) * (W // b)
         combined = temporal.expand(nW, T, T, wa, wa)
     # [nW, Tq, Tk, wa, wa] -> [nW, Tq, wa, Tk, wa] -> [nW, T*wa, T*wa]
-    return combined.permute(0, 1, 3, 2, 4).reshape(-1, T * wa, T * wa).contiguous()
+    m = combined.permute(0, 1, 3, 2, 4).reshape(-1, T * wa, T * wa).contiguous()
+    return m if device is None else m.to(device)
 
 
 # ----------------------------------------------------------------------------
@@ -118,10 +121,12 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: Optional[float] = None)
     return x * torch.rsqrt(ms + eps) * weight
 
 
-def gelu_erf(x: torch.Tensor) -> torch.Tensor:
+def gelu_erf(x: torch.Tensor, approximate: str = "none") -> torch.Tensor:
     """``nn.GELU()`` default (approximate='none'), models/mlp.py:55,82: the
-    library routine the reference calls, x * Phi(x) with the exact erf."""
-    return F.gelu(x)
+    library routine the reference calls, x * Phi(x) with the exact erf.
+    ``approximate="tanh"``: the tanh form, the "gelu" activation of the TE
+    block's te.LayerNormMLP (models/swin_helpers_te.py:318-323)."""
+    return F.gelu(x, approximate=approximate)
 
 
 def window_attention(x: torch.Tensor, p: Dict[str, torch.Tensor], num_heads: int,
@@ -145,7 +150,9 @@ def window_attention(x: torch.Tensor, p: Dict[str, torch.Tensor], num_heads: int
     v = heads(F.linear(x, p["attn.v.weight"]) + p["attn.biasv.bias"])
     q = rms_norm(q, p["attn.q_norm.norm.weight"], eps)
     k = rms_norm(k, p["attn.k_norm.norm.weight"], eps)
-    scores = torch.matmul(q, k.transpose(-1, -2)) * (hd ** -0.5)
+    # k^T materialised: the same product, and no transposed-view operand in
+    # batched GPU matmuls when the oracle runs on a device
+    scores = torch.matmul(q, k.transpose(-1, -2).contiguous()) * (hd ** -0.5)
     if mask is not None:
         nW = mask.shape[0]
         m = mask[None].expand(Bw // nW, nW, L, L).reshape(Bw, 1, L, L)
@@ -157,11 +164,11 @@ def window_attention(x: torch.Tensor, p: Dict[str, torch.Tensor], num_heads: int
     return o + p["attn.biasproj.bias"]
 
 
-def mlp(x: torch.Tensor, p: Dict[str, torch.Tensor]) -> torch.Tensor:
+def mlp(x: torch.Tensor, p: Dict[str, torch.Tensor], gelu: str = "none") -> torch.Tensor:
     """``MLP.forward`` (models/mlp.py:75-95): fc1 -> +bias1 -> GELU(erf) ->
     dropout(identity) -> fc2 -> +bias2 (after the identity all-reduce)."""
     h = F.linear(x, p["mlp.fc1.weight"]) + p["mlp.bias1.bias"]
-    h = gelu_erf(h)
+    h = gelu_erf(h, gelu)
     y = F.linear(h, p["mlp.fc2.weight"])
     return y + p["mlp.bias2.bias"]
 
@@ -183,18 +190,21 @@ def shifted_window_attn(x: torch.Tensor, p: Dict[str, torch.Tensor], num_heads: 
 def block_forward(x: torch.Tensor, p: Dict[str, torch.Tensor], num_heads: int,
                   window_size: Tuple[int, int], shift_size: Tuple[int, int],
                   mask: Optional[torch.Tensor] = None,
-                  eps: Optional[float] = None) -> torch.Tensor:
+                  eps: Optional[float] = None, gelu: str = "none") -> torch.Tensor:
     """``Block.forward`` (models/swin_helpers.py:435-459): pre-norm residual
-    attention, then pre-norm residual MLP over [B, T*H*W, C]."""
+    attention, then pre-norm residual MLP over [B, T*H*W, C].  ``gelu`` and
+    ``eps`` = ("tanh", 1e-5) give the TE block's arithmetic
+    (models/swin_helpers_te.py:302, 318-323: te.RMSNorm / te.LayerNormMLP at
+    their default eps and TE's tanh-form "gelu")."""
     B, T, H, W, C = x.shape
     if mask is None:
-        mask = make_attention_mask(H, W, window_size, shift_size, T)
+        mask = make_attention_mask(H, W, window_size, shift_size, T, device=x.device)
     skip = x
     h = rms_norm(x, p["norm1.norm.weight"], eps)
     h = shifted_window_attn(h, p, num_heads, window_size, shift_size, mask, eps)
     x = h + skip
     x = x.reshape(B, -1, C)
-    y = mlp(rms_norm(x, p["norm2.norm.weight"], eps), p) + x
+    y = mlp(rms_norm(x, p["norm2.norm.weight"], eps), p, gelu) + x
     return y.reshape(B, T, H, W, C)
 
 

@@ -34,4 +34,8 @@ def device():
     import torch
     if not torch.cuda.is_available():
         pytest.fail("GPU test collected on a machine without a GPU; run with -m gpu on the GPU box")
+    # references evaluated on the device (full-size checks) use full fp32 products
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+    torch.set_float32_matmul_precision("highest")
     return torch.device("cuda:0")

@@ -33,13 +33,21 @@ def run_block(device, dtype, B, T, H, W, C, heads, ws, shift, seed=1, random_bia
         y = blk(x.to(device=device, dtype=dtype))
     torch.cuda.synchronize()
     eps = torch.finfo(dtype).eps
-    want = ref.block_forward(x, p, heads, ws, shift, eps=eps)
+    if B * T * H * W * C <= 4e6:
+        want = ref.block_forward(x, p, heads, ws, shift, eps=eps)
+    else:
+        # production width: the same oracle evaluated with fp32 library
+        # kernels on the device (TF32 off), returned on the CPU
+        pd = {k: v.to(device) for k, v in p.items()}
+        want = ref.block_forward(x.to(device), pd, heads, ws, shift, eps=eps).cpu()
     return x, y.float().cpu(), want
 
 
 FP32_CASES = [
     # B, T, H, W, C, heads, ws, shift   (config 1 first)
     (1, 1, 90, 180, 192, 6, (9, 18), (4, 9)),
+    (1, 1, 180, 360, 1024, 16, (9, 18), (4, 9)),   # config 2 geometry in fp32 (hd 64, fc2 K = 4096)
+    (1, 1, 180, 360, 1024, 16, (9, 18), (0, 0)),
     (1, 1, 90, 180, 192, 6, (9, 18), (0, 0)),
     (2, 1, 18, 36, 128, 2, (9, 18), (4, 9)),
     (1, 2, 18, 36, 128, 4, (9, 18), (4, 9)),

@@ -58,6 +58,7 @@ def test_rmsnorm_roll_partition(device, dtype):
 GEMM_SHAPES = [
     # M, N, K
     (64800, 1024, 1024),
+    (64800, 1024, 4096),  # fc2 at config 2 (128 stages)
     (1000, 576, 192),     # N not a multiple of the 128 tile, M tail
     (300, 192, 768),
     (257, 4096, 256),
@@ -70,19 +71,26 @@ GEMM_SHAPES = [
 ]
 
 
+def ref_linear(x, w, device):
+    """F.linear in fp32 (the library routine the reference calls), on the CPU
+    for small products and with the fp32 device GEMM (TF32 off) for large
+    ones, returned on the CPU."""
+    if x.shape[0] * w.shape[0] * x.shape[1] <= 2e10:
+        return F.linear(x.float(), w.float())
+    return F.linear(x.to(device).float(), w.to(device).float()).cpu()
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
 @pytest.mark.parametrize("epi", ["none", "bias", "gelu", "residual"])
 def test_linear_epilogues(device, dtype, M, N, K, epi):
     from nsw import _lib, ops
-    if dtype == torch.float32 and M * N * K > 1e11:
-        pytest.skip("fp32 CPU oracle too slow at this size")
     g = torch.Generator().manual_seed(M + N + K)
     x = torch.randn(M, K, generator=g).to(dtype)
     w = synth.trunc_normal((N, K), 0.02, g).to(dtype)
     b = (0.1 * torch.randn(N, generator=g)).to(dtype)
     r = torch.randn(M, N, generator=g).to(dtype)
-    lin = F.linear(x.float(), w.float())
+    lin = ref_linear(x, w, device)
     if epi == "none":
         got = ops.linear(x.to(device), w.to(device))
         want = lin
@@ -105,8 +113,6 @@ def test_linear_epilogues(device, dtype, M, N, K, epi):
 @pytest.mark.parametrize("M,C,heads", [(64800, 1024, 16), (16200, 192, 6), (500, 128, 8), (100, 64, 1)])
 def test_qkv_projection_headnorm(device, dtype, M, C, heads):
     from nsw import ops
-    if dtype == torch.float32 and M * C * C * 3 > 3e11:
-        pytest.skip("fp32 CPU oracle too slow at this size")
     hd = C // heads
     g = torch.Generator().manual_seed(7)
     x = torch.randn(M, C, generator=g).to(dtype)
@@ -116,7 +122,7 @@ def test_qkv_projection_headnorm(device, dtype, M, C, heads):
     kn = (1 + 0.2 * torch.randn(hd, generator=g)).to(dtype)
     eps = torch.finfo(dtype).eps
     got = ops.qkv_projection(x.to(device), w.to(device), b.to(device), qn.to(device), kn.to(device), heads, eps)
-    y = F.linear(x.float(), w.float()) + b.float()
+    y = ref_linear(x, w, device) + b.float()
     q, k, v = y.split(C, dim=-1)
     q = ref.rms_norm(q.reshape(M, heads, hd), qn.float(), eps).reshape(M, C)
     k = ref.rms_norm(k.reshape(M, heads, hd), kn.float(), eps).reshape(M, C)

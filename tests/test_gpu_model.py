@@ -218,21 +218,25 @@ def test_model_config3_channels_bf16(device):
     assert rel_l2(got, want) < 1e-2
 
 
+@pytest.mark.parametrize("sd", [torch.float32, torch.float64])
 @pytest.mark.parametrize("pd", [torch.float32, torch.bfloat16])
-def test_metrics_unnorm_vs_oracle(device, pd):
+def test_metrics_unnorm_vs_oracle(device, pd, sd):
     import nsw
     B, T, C, H, W = 1, 1, 5, 90, 180
     g = torch.Generator().manual_seed(23)
     gen = torch.randn(B, T, C, H, W, generator=g).to(pd)
     tgt = torch.randn(B, T, C, H, W, generator=g)
-    std = torch.rand(C, generator=g) + 0.5
-    mean = torch.randn(C, generator=g) * 10
+    std = (torch.rand(C, generator=g, dtype=torch.float64) + 0.5).to(sd)
+    mean = (torch.randn(C, generator=g, dtype=torch.float64) * 10).to(sd)
     clim = torch.randn(C, generator=g) * 10
     w = torch.from_numpy(metrics_ref.area_weights(metrics_ref.era5_latitudes(H)))
     r, a = nsw.ops.weighted_metrics_unnorm(gen.to(device), tgt.to(device), std, mean, w[:, None], clim)
-    # reference: separate product and sum in fp32, then the metrics in float64
+    # reference: separate product and sum with torch's type promotion (fp32
+    # fields with fp32 stats stay fp32, float64 stats promote them), then the
+    # metrics in float64
     pred = (gen.float() * std.view(1, 1, C, 1, 1)) + mean.view(1, 1, C, 1, 1)
     targ = (tgt * std.view(1, 1, C, 1, 1)) + mean.view(1, 1, C, 1, 1)
+    assert pred.dtype == sd
     wr = metrics_ref.weighted_rmse(pred.double().numpy(), targ.double().numpy(), w.numpy(), True)
     wa = metrics_ref.weighted_acc(pred.double().numpy(), targ.double().numpy(), w.numpy(), clim.double().numpy(),
                                   True)

@@ -87,6 +87,65 @@ def test_mlp_rejects_unfusable_activation():
     m = MLP(16, 32, act_layer=torch.nn.ReLU)
     with pytest.raises(NotImplementedError):
         m._check_fusable()
+    t = MLP(16, 32, act_layer=lambda: torch.nn.GELU(approximate="tanh"))
+    t._check_fusable()
+    assert t.gelu_tanh
+
+
+@pytest.mark.parametrize("H,W,ws,shift,T", [(18, 36, (9, 18), (4, 9), 1), (18, 36, (9, 18), (4, 9), 2),
+                                            (18, 36, (9, 18), (0, 0), 1), (18, 36, (9, 18), (0, 9), 1),
+                                            (16, 32, (4, 8), (2, 4), 1), (24, 16, (4, 8), (6, 4), 1)])
+def test_block_attn_mask_buffer_at_construction(H, W, ws, shift, T):
+    """The reference registers attn_mask as a non-persistent buffer when the
+    block is built (models/swin_helpers.py:320,397): available on the CPU,
+    equal to the oracle's mask, absent from the state dict, moved and cast
+    with the module."""
+    import nsw
+    from oracle import swin_ref
+    blk = nsw.Block(dim=64, num_heads=2, feat_size=(H, W), window_size=ws, temporal_context_window_size=T,
+                    shift_size=shift)
+    assert blk.attn_mask.device.type == "cpu" and blk.attn_mask.dtype == torch.float32
+    assert torch.equal(blk.attn_mask, swin_ref.make_attention_mask(H, W, ws, shift, T))
+    assert "attn_mask" not in blk.state_dict()
+    assert torch.equal(blk.to(torch.bfloat16).attn_mask.float(), swin_ref.make_attention_mask(H, W, ws, shift, T))
+
+
+def test_apply_te_semantics():
+    """TE-layout checkpoints switch the blocks to the TE arithmetic: eps 1e-5
+    on all four RMSNorms and the tanh-form GELU (models/swin_helpers_te.py)."""
+    import nsw
+    from nsw import checkpoint
+    meta = {"coords": torch.rand(36, 72, 3), "sp_shapes": [[36], [72]], "n_channels": 4}
+    model = nsw.SwinTransformer(temporal_context_window_size=1, window_size=(9, 18), patch_size=2, in_chans=4,
+                                out_chans=4, embed_dim=64, depth=2, num_heads=2, domain_metadata=meta)
+    assert checkpoint.apply_te_semantics(model) == 2
+    for blk in model.blocks:
+        assert blk._eps(torch.bfloat16) == 1e-5 and blk._eps(torch.float32) == 1e-5
+        assert blk.mlp.gelu_tanh
+
+
+def test_load_model_checkpoint_te_and_vanilla(tmp_path):
+    import nsw
+    from nsw import checkpoint
+    from oracle import synth
+    C, E, depth, heads, p, H, W = 4, 64, 2, 2, 2, 36, 72
+    meta = {"coords": torch.rand(H, W, 3), "sp_shapes": [[H], [W]], "n_channels": C}
+
+    def mk():
+        return nsw.SwinTransformer(temporal_context_window_size=1, window_size=(9, 18), patch_size=p, in_chans=C,
+                                   out_chans=C, embed_dim=E, depth=depth, num_heads=heads, domain_metadata=meta)
+    prm = synth.model_params(C, C, E, depth, heads, p, seed=5)
+    torch.save({"model_state": {"module.model." + k: v for k, v in checkpoint.vanilla_to_te(prm).items()}},
+               tmp_path / "te.tar")
+    torch.save({"model_state": {"module." + k: v for k, v in prm.items()}}, tmp_path / "van.tar")
+    m = mk()
+    _, _, te = checkpoint.load_model_checkpoint(m, str(tmp_path / "te.tar"))
+    assert te and all(b.mlp.gelu_tanh for b in m.blocks)
+    m2 = mk()
+    _, _, te2 = checkpoint.load_model_checkpoint(m2, str(tmp_path / "van.tar"))
+    assert not te2 and not any(b.mlp.gelu_tanh for b in m2.blocks)
+    for k, v in prm.items():
+        assert torch.equal(m.state_dict()[k], v) and torch.equal(m2.state_dict()[k], v), k
 
 
 def test_full_model_te_checkpoint_loads_into_swin_transformer(tmp_path):

@@ -42,6 +42,18 @@ def test_gelu_matches_nn_gelu():
     assert (ref.gelu_erf(x).double() - exact).abs().max().item() < 2e-6
 
 
+def test_gelu_tanh_form_closed_form():
+    """The TE block's "gelu" is the tanh form 0.5 x (1 + tanh(sqrt(2/pi)
+    (x + 0.044715 x^3))); the oracle's option reproduces that closed form in
+    float64 and differs from the erf form by its known ~1e-3 amount."""
+    x = torch.linspace(-8, 8, 1001)
+    xd = x.double()
+    closed = 0.5 * xd * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (xd + 0.044715 * xd ** 3)))
+    assert (ref.gelu_erf(x, "tanh").double() - closed).abs().max().item() < 2e-6
+    d = (ref.gelu_erf(x, "tanh") - ref.gelu_erf(x)).abs().max().item()
+    assert 1e-4 < d < 1e-2
+
+
 def test_attention_core_matches_sdpa():
     torch.manual_seed(0)
     C, heads, L = 32, 4, 24

@@ -23,6 +23,20 @@ def test_patch_conv_is_im2col_product():
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
 
 
+def test_patch_conv_unfold_form():
+    """The device form of the patch convolution (unfold x weight) against
+    F.conv2d and against the brute-force im2col product."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 6, 12, 20, generator=g)
+    w = torch.randn(9, 6, 4, 4, generator=g)
+    b = torch.randn(9, generator=g)
+    got = mr.patch_conv_unfold(x, w, b, 4)
+    torch.testing.assert_close(got, F.conv2d(x, w, b, stride=4), rtol=1e-5, atol=1e-5)
+    cols = mr.im2col_bruteforce(x, 4)
+    want = (cols @ w.reshape(9, -1).T + b).view(2, 3, 5, 9).permute(0, 3, 1, 2)
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+
+
 def test_head_unpatchify_matches_elementwise_loop():
     g = torch.Generator().manual_seed(1)
     b, t, h, w, E, p, c = 2, 2, 3, 4, 8, 2, 3
