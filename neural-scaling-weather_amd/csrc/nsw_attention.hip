@@ -347,8 +347,11 @@ __global__ __launch_bounds__(256) void attn_scalar_kernel(AttnArgs a) {
         for (int d = 0; d < HD; ++d) s += qv[d] * Kc[kk][d];
         if (a.mask_mode != MASK_NONE) s += mask_value(a, win, qc, k0 + kk, last_band);
         const float mn = fmaxf(m, s);
-        const float corr = expf(m - mn);
-        const float p = expf(s - mn);
+        // offsets taken from 0 while every logit so far is -inf (keys masked
+        // by -inf): exp(-inf) = 0 instead of exp(-inf - -inf) = NaN
+        const float mo = mn == -INFINITY ? 0.f : mn;
+        const float corr = expf(m - mo);
+        const float p = expf(s - mo);
         l = l * corr + p;
 #pragma unroll
         for (int d = 0; d < HD; ++d) acc[d] = acc[d] * corr + p * Vc[kk][d];

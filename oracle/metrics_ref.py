@@ -33,29 +33,33 @@ def area_weights(latitudes: np.ndarray) -> np.ndarray:
 
 
 def weighted_sums(pred: np.ndarray, target: np.ndarray, w_lat: np.ndarray,
-                  clim: np.ndarray | None = None) -> np.ndarray:
+                  clim: np.ndarray | None = None, field_dtype=np.float32) -> np.ndarray:
     """Per (b, t, c) plane: [sum w*(p-t)^2, sum w*af*ao, sum w*af^2, sum w*ao^2]
-    (float64).  pred/target [B,T,C,H,W] float32; w_lat [H]; clim [C] or None."""
-    p = pred.astype(np.float32)
-    t = target.astype(np.float32)
-    d = (p - t).astype(np.float32)
-    se = (d * d).astype(np.float32).astype(np.float64)
+    (float64).  pred/target [B,T,C,H,W] holding values of ``field_dtype``
+    (float32 fields, or float64 ones when float64 statistics promoted them),
+    in which the difference and its square are formed; w_lat [H]; clim [C]
+    or None."""
+    fd = np.dtype(field_dtype)
+    p = pred.astype(fd)
+    t = target.astype(fd)
+    d = (p - t).astype(fd)
+    se = (d * d).astype(fd).astype(np.float64)
     w = w_lat.astype(np.float64)[:, None]
     out = np.zeros(pred.shape[:3] + (4,), dtype=np.float64)
     out[..., 0] = (se * w).sum(axis=(-1, -2))
     if clim is not None:
-        cl = clim.astype(np.float32)[None, None, :, None, None]
-        af = (p - cl).astype(np.float32).astype(np.float64)
-        ao = (t - cl).astype(np.float32).astype(np.float64)
+        cl = clim.astype(fd)[None, None, :, None, None]
+        af = (p - cl).astype(fd).astype(np.float64)
+        ao = (t - cl).astype(fd).astype(np.float64)
         out[..., 1] = (w * af * ao).sum(axis=(-1, -2))
         out[..., 2] = (w * af * af).sum(axis=(-1, -2))
         out[..., 3] = (w * ao * ao).sum(axis=(-1, -2))
     return out
 
 
-def weighted_rmse(pred, target, w_lat, temporal_average: bool = True) -> np.ndarray:
+def weighted_rmse(pred, target, w_lat, temporal_average: bool = True, field_dtype=np.float32) -> np.ndarray:
     H, W = pred.shape[-2:]
-    s = weighted_sums(pred, target, w_lat)[..., 0]
+    s = weighted_sums(pred, target, w_lat, field_dtype=field_dtype)[..., 0]
     rmse = np.sqrt(s / float(H * W))        # [B, T, C]
     if temporal_average:
         while rmse.ndim > 1:
@@ -64,8 +68,8 @@ def weighted_rmse(pred, target, w_lat, temporal_average: bool = True) -> np.ndar
     return rmse.mean(axis=0)
 
 
-def weighted_acc(pred, target, w_lat, clim, temporal_average: bool = True) -> np.ndarray:
-    s = weighted_sums(pred, target, w_lat, clim)
+def weighted_acc(pred, target, w_lat, clim, temporal_average: bool = True, field_dtype=np.float32) -> np.ndarray:
+    s = weighted_sums(pred, target, w_lat, clim, field_dtype=field_dtype)
     acc = s[..., 1] / np.sqrt(s[..., 2] * s[..., 3])
     if temporal_average:
         while acc.ndim > 1:

@@ -237,9 +237,10 @@ def test_metrics_unnorm_vs_oracle(device, pd, sd):
     pred = (gen.float() * std.view(1, 1, C, 1, 1)) + mean.view(1, 1, C, 1, 1)
     targ = (tgt * std.view(1, 1, C, 1, 1)) + mean.view(1, 1, C, 1, 1)
     assert pred.dtype == sd
-    wr = metrics_ref.weighted_rmse(pred.double().numpy(), targ.double().numpy(), w.numpy(), True)
+    fd = np.float64 if sd == torch.float64 else np.float32
+    wr = metrics_ref.weighted_rmse(pred.double().numpy(), targ.double().numpy(), w.numpy(), True, field_dtype=fd)
     wa = metrics_ref.weighted_acc(pred.double().numpy(), targ.double().numpy(), w.numpy(), clim.double().numpy(),
-                                  True)
+                                  True, field_dtype=fd)
     np.testing.assert_allclose(r.cpu().numpy()[0, 0], wr, rtol=1e-10)
     np.testing.assert_allclose(a.cpu().numpy()[0, 0], wa, rtol=1e-9, atol=1e-12)
 

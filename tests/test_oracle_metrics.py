@@ -48,3 +48,24 @@ def test_acc_special_cases():
     assert np.allclose(mr.weighted_acc(f, f, w, clim), 1.0, atol=1e-12)
     o = (2 * clim[None, None, :, None, None] - f).astype(np.float32)
     assert np.allclose(mr.weighted_acc(f, o, w, clim), -1.0, atol=1e-6)
+
+
+def test_float64_fields_keep_float64_differences():
+    """With float64 fields (float64 statistics promote the unnormalised
+    fields) the squared differences are formed in float64: a float64 offset
+    that float32 cannot hold is recovered exactly, and the sums equal a
+    float64 loop."""
+    rng = np.random.default_rng(3)
+    B, T, C, H, W = 1, 1, 2, 4, 6
+    p = rng.standard_normal((B, T, C, H, W)) * 10
+    d = 1e-9
+    w = mr.area_weights(mr.era5_latitudes(H))
+    r64 = mr.weighted_rmse(p + d, p, w, field_dtype=np.float64)
+    assert np.allclose(r64, d, rtol=1e-4, atol=0)
+    assert not np.allclose(mr.weighted_rmse(p + d, p, w), d, rtol=1e-4, atol=0)     # float32 fields lose it
+    t = rng.standard_normal((B, T, C, H, W))
+    s = mr.weighted_sums(p, t, w, field_dtype=np.float64)[..., 0]
+    brute = np.zeros((B, T, C))
+    for c in range(C):
+        brute[0, 0, c] = sum(w[h] * (p[0, 0, c, h, x] - t[0, 0, c, h, x]) ** 2 for h in range(H) for x in range(W))
+    assert np.allclose(s, brute, rtol=1e-13)
