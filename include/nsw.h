@@ -242,6 +242,21 @@ int nsw_weighted_metrics_unnorm_f64stats(const void* pred, int pred_dtype, const
                                          int64_t Cch, double* rmse, double* acc, void* workspace,
                                          size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of nsw_weighted_metrics_unnorm.  No counterpart in
+ * the reference: for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops).  Same arguments without the workspace; the
+ * partial sums live in a library-owned device array of
+ * NSW_METRICS_SCRATCH_BYTES per GPU (held until the process ends), enough
+ * for nsw_weighted_metrics_workspace_size(P, H, W) <= that size (e.g. every
+ * P <= 32768 planes); larger inputs return NSW_ERR_INVALID.  The stream must
+ * belong to the current device.  Calls that overlap on one GPU share the
+ * array and race; calls in one stream's order are safe. */
+#define NSW_METRICS_SCRATCH_BYTES (1 << 20)
+int nsw_weighted_metrics_unnorm_noalloc(const void* pred, int pred_dtype, const float* target,
+                                        const float* std_c, const float* mean_c, const double* w,
+                                        int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
+                                        int64_t Cch, double* rmse, double* acc, void* stream);
+
 /* Block.forward's first half with norm1 fused (models/swin_helpers.py:446 +
  * :402-412 + WindowMultiHeadAttention.forward :212-241): qkv[m] (window order,
  * [B*nW*T*wa, 3C]) = per-head-q/k-RMSNorm(rs[t] * (x[t] . wqkv_n^T) + bqkv) with

@@ -7,6 +7,8 @@
 // and sum).  A second tiny kernel adds the bands of each plane in a fixed
 // order (deterministic; no atomics) and finishes rmse / acc.  HBM-bound:
 // 8 bytes read per grid point.
+#include <mutex>
+
 #include "nsw_common.h"
 
 namespace nsw {
@@ -221,5 +223,76 @@ extern "C" int nsw_weighted_metrics_unnorm_f64stats(const void* pred, int pred_d
   if (pred_dtype == NSW_DTYPE_BF16)
     return run_metrics<bf16, double, true>((const bf16*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W,
                                            Cch, rmse, acc, workspace, workspace_bytes, st, what);
+  return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, pred_dtype);
+}
+
+// ------------------------------------------------ allocation-free variant ----
+// nsw_weighted_metrics_unnorm_noalloc keeps its per-(plane, band) partial sums
+// in `scratch`, a device global of NSW_METRICS_SCRATCH_BYTES: each GPU the
+// library runs on holds one copy until the process ends.  In host code the
+// name `scratch` is only a handle; the device address of a GPU's copy comes
+// from hipGetSymbolAddress with that GPU current, looked up on the first call
+// on each device and kept per device.  Nothing in it has to start at zero
+// (every partial the final kernel reads is written by the partial kernel of
+// the same call), and it keeps the last call's contents.  Calls that overlap
+// on one GPU (different streams, or other host threads) share the array and
+// race; calls in stream order do not.
+namespace nsw {
+
+static __device__ __align__(256) double scratch[NSW_METRICS_SCRATCH_BYTES / sizeof(double)];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_address(hipStream_t st, void** out, const char* what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(NSW_ERR_HIP, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+  if (st != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(st, &sdev);
+    if (e != hipSuccess) return set_error(NSW_ERR_HIP, "%s: hipStreamGetDevice: %s", what, hipGetErrorString(e));
+    NSW_CHECK_ARG((int)sdev == dev, "%s: the stream belongs to device %d, the current device is %d", what,
+                  (int)sdev, dev);
+  }
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(NSW_ERR_UNSUPPORTED, "%s: device %d beyond the %d supported", what, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(NSW_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NSW_OK;
+}
+
+}  // namespace nsw
+
+extern "C" int nsw_weighted_metrics_unnorm_noalloc(const void* pred, int pred_dtype, const float* target,
+                                                   const float* std_c, const float* mean_c, const double* w,
+                                                   int64_t w_cols, const float* clim, int64_t P, int64_t H,
+                                                   int64_t W, int64_t Cch, double* rmse, double* acc,
+                                                   void* stream) {
+  const char* what = "nsw_weighted_metrics_unnorm_noalloc";
+  NSW_CHECK_ARG(P > 0 && H > 0 && W > 0, "%s: P, H, W must be positive", what);
+  const size_t need = nsw_weighted_metrics_workspace_size(P, H, W);
+  NSW_CHECK_ARG(need <= (size_t)NSW_METRICS_SCRATCH_BYTES,
+                "%s: %lld planes of %lld rows need %zu bytes of partial sums, more than the %d-byte scratch", what,
+                (long long)P, (long long)H, need, (int)NSW_METRICS_SCRATCH_BYTES);
+  hipStream_t st = (hipStream_t)stream;
+  void* ptr = nullptr;
+  int rc = scratch_address(st, &ptr, what);
+  if (rc) return rc;
+  if (pred_dtype == NSW_DTYPE_F32)
+    return run_metrics<float, float, true>((const float*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W,
+                                           Cch, rmse, acc, ptr, NSW_METRICS_SCRATCH_BYTES, st, what);
+  if (pred_dtype == NSW_DTYPE_BF16)
+    return run_metrics<bf16, float, true>((const bf16*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W,
+                                          Cch, rmse, acc, ptr, NSW_METRICS_SCRATCH_BYTES, st, what);
   return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, pred_dtype);
 }

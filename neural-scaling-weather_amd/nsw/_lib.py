@@ -24,6 +24,7 @@ NSW_EPI_BIAS = 1
 NSW_EPI_BIAS_GELU = 2
 NSW_EPI_BIAS_RESIDUAL = 3
 NSW_EPI_BIAS_GELU_TANH = 4
+NSW_METRICS_SCRATCH_BYTES = 1 << 20   # scratch of nsw_weighted_metrics_unnorm_noalloc (per GPU)
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -76,6 +77,8 @@ SIGNATURES = {
                                            _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "nsw_weighted_metrics_unnorm_f64stats": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
                                                     _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "nsw_weighted_metrics_unnorm_noalloc": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
+                                                   _i64, _vp, _vp, _vp]),
     "nsw_qkv_projection_norm_gather": (_int, [_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _i64, _i64, _i64, _i64,
                                               _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "nsw_linear_rownorm": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _f32, _int, _vp]),
