@@ -10,7 +10,12 @@ dominant kernel from HIP events on the launch stream, the per-kernel
 breakdown, and a CPU baseline (the fp32 oracle on the host cores, on a
 bounded sample of the same workload).  One GPU only.
 
-Unless --no-model is given the line also carries
+The line also carries
+  "kernels.metrics_unnorm": the config-5 per-step RMSE/ACC reduction (HBM);
+  "gemm_vs_hipblaslt": the block's four GEMM shapes without epilogue, this
+              library's GEMM against torch.matmul (hipBLASLt), same operands;
+  "config4":  the config-4 block and one forward of the depth-8 p2 model;
+and, unless --no-model is given,
   "forecast": config 3, one SwinTransformer forward (p4, e1024, depth 16,
               16 heads, window 9x18, 70 channels, 720x1440, bf16) = ms per
               forecast step, split into embedding / blocks / head;
@@ -19,6 +24,11 @@ Unless --no-model is given the line also carries
               against the same weights in fp32: per-step drift.
 Inputs there are seeded Gaussian-filtered, per-channel standardised fields
 (sigma = 8 px), standing in for ERA5.
+
+Traffic (roofline.traffic): profile this command with --copy-calibration
+under two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE) and summarise
+them with --traffic-summary; the calibration copy and the block's kernels
+then come from the same runs.
 """
 from __future__ import annotations
 
@@ -85,18 +95,19 @@ def main():
                          "separate: both norms as passes of their own, 7 launches")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a plain 256 MiB device copy (5 launches): the reference kernel whose "
-                         "FETCH_SIZE / WRITE_SIZE counters calibrate the HBM-traffic figures")
+                    help="before anything else, run a plain 256 MiB device copy (5 launches): the "
+                         "reference kernel whose FETCH_SIZE / WRITE_SIZE counters, read in the same "
+                         "rocprofv3 --pmc run as the block's kernels, calibrate the HBM-traffic figures")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="no GPU work: read the counter CSVs of a FETCH_SIZE and a WRITE_SIZE rocprofv3 run "
+                         "of 'bench.py --copy-calibration ...', print the calibrated traffic per kernel as "
+                         "markdown and write profiles/traffic_<config>.json")
+    ap.add_argument("--no-config4", action="store_true", help="skip the config-4 block and model timing")
+    ap.add_argument("--no-gemm-compare", action="store_true", help="skip the hipBLASLt comparison leg")
     args = ap.parse_args()
 
-    if args.copy_calibration:
-        import torch
-        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration_bytes": src.numel(), "launches": 5}), flush=True)
+    if args.traffic_summary:
+        traffic_summary(args.traffic_summary[0], args.traffic_summary[1], args.config)
         return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -109,6 +120,9 @@ def main():
     import torch
     import nsw
     from nsw import _lib, ops
+
+    if args.copy_calibration:
+        copy_calibration()
 
     B, T, H, W, C, heads, ws, shift, dts, desc = CONFIGS[args.config]
     dtype = torch.bfloat16 if dts == "bf16" else torch.float32
@@ -259,9 +273,20 @@ def main():
         "kernels": kern,
     }
 
+    # ----------------------------------------- metrics kernel (config 5 step)
+    kern["metrics_unnorm"] = metrics_timing(dev, args.steps, args.warmup)
+    # ------------------------------------------------ GEMMs against hipBLASLt
+    if not args.no_gemm_compare and args.config in ("c2", "c2u"):
+        out["gemm_vs_hipblaslt"] = gemm_compare(dev, M, C, 4 * C, args.steps, args.warmup)
+    # ------------------------------------------------------------ config 4
+    if not args.no_config4 and args.config in ("c2", "c2u"):
+        del st
+        torch.cuda.empty_cache()
+        out["config4"] = config4_section(dev, args.steps, args.warmup, args.model_steps)
+
     # ------------------------------------------------- config 3 / config 5
     if not args.no_model:
-        del y, y2, st
+        del y, y2
         torch.cuda.empty_cache()
         out["forecast"], rollout = model_sections(dev, args.model_steps, args.warmup, not args.no_rollout)
         if rollout is not None:
@@ -271,6 +296,189 @@ def main():
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, args.cpu_seconds)
     print(json.dumps(out), flush=True)
+
+
+def copy_calibration():
+    """A plain 256 MiB device-to-device copy, 5 launches: its FETCH_SIZE /
+    WRITE_SIZE per dispatch divided by the bytes it moves is the factor that
+    turns those counters into HBM bytes for the other kernels of the same
+    profiled run."""
+    import torch
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": src.numel(), "launches": 5}), flush=True)
+    del src, dst
+    torch.cuda.empty_cache()
+
+
+# Kernel names in a rocprofv3 trace -> bench.py's kernel names (config 2,
+# bf16, the default 6-launch block).  The GEMM instances are told apart by
+# their (mangled) template arguments: gemm_kernel<T, EPI, PRE>.
+TRACE_NAMES = [
+    ("_ZN3nsw11gemm_kernelIDF16bLi2ELi3E", "fc1_rowscale"),
+    ("_ZN3nsw11gemm_kernelIDF16bLi3ELi0E", "fc2"),
+    ("_ZN3nsw11gemm_kernelIDF16bLi64ELi0E", "qkv"),
+    ("_ZN3nsw11gemm_kernelIDF16bLi11ELi0E", "proj_scatter_sumsq"),
+    ("attn_mfma_kernel", "attention"),
+    ("row_map_kernel", "gather_norm1"),
+    ("wsum_partial_kernel", "metrics_unnorm"),
+    ("__amd_rocclr_copyBuffer", "copy_calibration"),
+]
+
+
+def trace_name(kernel_name):
+    for key, name in TRACE_NAMES:
+        if kernel_name.startswith(key) or key in kernel_name:
+            return name
+    return None
+
+
+def traffic_summary(fetch_dir, write_dir, config):
+    """Calibrated HBM traffic per kernel from two rocprofv3 --pmc runs (one
+    counter each) of the same bench command with --copy-calibration: the
+    counters (KB per dispatch) are scaled by what they read for the 256 MiB
+    copy of that run."""
+    import csv
+    import glob
+
+    def load(d, counter):
+        acc = {}
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for r in csv.DictReader(f):
+                    if r["Counter_Name"] != counter:
+                        continue
+                    n = trace_name(r["Kernel_Name"])
+                    if n is not None:
+                        acc.setdefault(n, []).append(float(r["Counter_Value"]) * 1024.0)
+        return {k: sum(v) / len(v) for k, v in acc.items()}
+
+    fetch, write = load(fetch_dir, "FETCH_SIZE"), load(write_dir, "WRITE_SIZE")
+    if "copy_calibration" not in fetch or "copy_calibration" not in write:
+        raise SystemExit("the runs hold no calibration copy: profile 'bench.py --copy-calibration ...'")
+    nbytes = float(256 << 20)
+    kf, kw = fetch["copy_calibration"] / nbytes, write["copy_calibration"] / nbytes
+    out = {}
+    rows = []
+    for n in sorted(set(fetch) & set(write)):
+        if n == "copy_calibration":
+            continue
+        f, w = fetch[n] / kf, write[n] / kw
+        out[n] = int(round(f + w))
+        rows.append(f"| {n} | {f / 1e6:.1f} | {w / 1e6:.1f} | {(f + w) / 1e6:.1f} |")
+    print(f"calibration (same runs): FETCH_SIZE reads {kf:.4f} x and WRITE_SIZE {kw:.4f} x the copy's bytes")
+    print("| kernel | fetch (MB) | write (MB) | total (MB) |\n|---|---|---|---|")
+    print("\n".join(rows))
+    out["_calibration"] = {"fetch_factor": round(kf, 4), "write_factor": round(kw, 4)}
+    with open(os.path.join(ROOT, "profiles", f"traffic_{config}.json"), "w") as fh:
+        json.dump(out, fh, indent=1, sort_keys=True)
+
+
+def timed(fn, steps, warmup):
+    """Mean ms of fn() between HIP events on the launch stream (a spin
+    kernel ahead of the first event hides the host's enqueue latency)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(SPIN_CYCLES)
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def metrics_timing(dev, steps, warmup):
+    """The rollout's per-step metric call at config 5 (70 channels,
+    720 x 1440, fp32 prediction and target, unnormalised RMSE + ACC): HBM
+    bound, 2 x 290.3 MB read per call (utils/losses.py:243-257)."""
+    import torch
+    import nsw
+    from nsw import ops
+    C, H, W = 70, 720, 1440
+    g = torch.Generator(device=dev).manual_seed(4001)
+    pred = torch.randn(1, 1, C, H, W, generator=g, device=dev)
+    tgt = torch.randn(1, 1, C, H, W, generator=g, device=dev)
+    std = torch.rand(C, generator=g, device=dev) + 0.5
+    mean = torch.randn(C, generator=g, device=dev)
+    clim = torch.randn(C, generator=g, device=dev)
+    lat = nsw.misc_utils.era5_latitudes(H)
+    w = nsw.build_spherical_area_weights(lat)[:, None].to(dev)
+    ms = timed(lambda: ops.weighted_metrics_unnorm(pred, tgt, std, mean, w, clim), steps, warmup)
+    nbytes = 2 * C * H * W * 4
+    ach = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "bound": "hbm", "achieved": round(ach, 1), "unit": "GB/s",
+            "frac": round(ach / PEAK_HBM_GBS, 4), "bytes": nbytes,
+            "workload": "config 5 per-step metrics: [1,1,70,720,1440] fp32 prediction and target, "
+                        "unnormalise + weighted RMSE + ACC (two launches: partial sums, final)"}
+
+
+def gemm_compare(dev, M, C, Hm, steps, warmup):
+    """The block's four GEMM shapes without epilogue, nsw_linear against
+    torch.matmul (hipBLASLt) on the same bf16 operands, interleaved."""
+    import torch
+    from nsw import ops
+    g = torch.Generator(device=dev).manual_seed(4101)
+    res = {}
+    for name, (N, K) in {"qkv": (3 * C, C), "proj": (C, C), "fc1": (Hm, C), "fc2": (C, Hm)}.items():
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        wt = w.t()
+        t_nsw, t_lib = [], []
+        for _ in range(3):
+            t_nsw.append(timed(lambda: ops.linear(x, w), steps, warmup))
+            t_lib.append(timed(lambda: torch.matmul(x, wt), steps, warmup))
+        a, b = ops.linear(x, w), torch.matmul(x, wt)
+        diff = (a.float() - b.float()).abs().max().item()
+        fl = 2.0 * M * N * K
+        tn, tl = min(t_nsw), min(t_lib)
+        res[name] = {"M": M, "N": N, "K": K, "nsw_ms": round(tn, 4), "hipblaslt_ms": round(tl, 4),
+                     "nsw_tflops": round(fl / (tn * 1e-3) / 1e12, 1), "hipblaslt_tflops": round(fl / (tl * 1e-3) / 1e12, 1),
+                     "max_abs_diff": diff}
+        del x, w, wt, a, b
+    return res
+
+
+def config4_section(dev, steps, warmup, model_steps):
+    """Config 4: the shifted block (360 x 720 tokens, C = 512, 8 heads) and
+    one forward of the depth-8 p2 model on 720 x 1440 x 70 (bf16)."""
+    import torch
+    import nsw
+    B, T, H, W, C, heads, ws, shift, dts, desc = CONFIGS["c4"]
+    torch.manual_seed(5001)
+    blk = nsw.Block(C, heads, (H, W), ws, T, shift_size=shift).to(device=dev, dtype=torch.bfloat16).eval()
+    x = torch.randn(B, T, H, W, C, device=dev).to(torch.bfloat16)
+    fl = block_flops(B, T, H, W, C, heads, ws)
+    with torch.inference_mode():
+        ms_blk = timed(lambda: blk(x), steps, warmup)
+    del blk, x
+    Cc, Hi, Wi, p, depth = 70, 720, 1440, 2, 8
+    lat = nsw.misc_utils.era5_latitudes(Hi)
+    lon = nsw.misc_utils.era5_longitudes(Wi)
+    meta = {"coords": nsw.get_spatial_coords((lat, lon)).float(), "sp_shapes": [[Hi], [Wi]], "n_channels": Cc}
+    model = nsw.SwinTransformer(temporal_context_window_size=T, window_size=ws, patch_size=p, in_chans=Cc,
+                                out_chans=Cc, embed_dim=C, depth=depth, num_heads=heads, coord_pos_embed=True,
+                                domain_metadata=meta).to(device=dev, dtype=torch.bfloat16).eval()
+    xm = smooth_fields((1, T, Cc, Hi, Wi), 8.0, 5002, dev)
+    tokens = (Hi // p) * (Wi // p)
+    step_flops = depth * sum(fl.values()) + 2 * tokens * (Cc * p * p) * C * 2
+    with torch.inference_mode():
+        ms_model = timed(lambda: model(xm), model_steps, warmup)
+        ok = bool(torch.isfinite(model(xm).float()).all())
+    del model, xm
+    torch.cuda.empty_cache()
+    return {"workload": desc + "; model: p2 e512 depth 8, 8 heads, 70 channels on 720x1440, bf16",
+            "block_ms": round(ms_blk, 4), "block_tokens_per_s": round(H * W / (ms_blk * 1e-3), 1),
+            "block_tflops": round(sum(fl.values()) / (ms_blk * 1e-3) / 1e12, 1),
+            "model_ms_per_step": round(ms_model, 3), "model_tflop_per_step": round(step_flops / 1e12, 3),
+            "model_tflops": round(step_flops / (ms_model * 1e-3) / 1e12, 1), "finite": ok}
 
 
 def smooth_fields(shape, sigma, seed, dev):
@@ -373,6 +581,8 @@ def model_sections(dev, steps, warmup, with_rollout=True):
     rollout = {
         "workload": "config 5: config-3 model, 8 autoregressive steps from one seeded initial condition, "
                     "per-step latitude-weighted RMSE and ACC over 70 channels (unnormalised fields)",
+        "drift_reference": "the same weights through this library's fp32 path; the drift against the fp32 "
+                           "oracle rollout is checked by tests/test_gpu_fullsize.py::test_rollout_config5",
         "steps": S, "ms_per_step_bf16": round(msb, 3), "ms_per_step_fp32": round(msf, 3),
         "rmse_mean_bf16": [round(float(v), 6) for v in rb.mean(1)],
         "rmse_rel_drift_max": [round(float(v), 6) for v in (np.abs(rb - rf) / rf).max(1)],
