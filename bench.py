@@ -353,8 +353,13 @@ def traffic_summary(fetch_dir, write_dir, config):
                         continue
                     n = trace_name(r["Kernel_Name"])
                     if n is not None:
-                        acc.setdefault(n, []).append(float(r["Counter_Value"]) * 1024.0)
-        return {k: sum(v) / len(v) for k, v in acc.items()}
+                        acc.setdefault(n, []).append((int(r["Grid_Size"]), float(r["Counter_Value"]) * 1024.0))
+        # the calibration copies are the largest copy dispatches (torch's other
+        # small copies use the same blit kernel)
+        if "copy_calibration" in acc:
+            gmax = max(g for g, _ in acc["copy_calibration"])
+            acc["copy_calibration"] = [(g, v) for g, v in acc["copy_calibration"] if g == gmax]
+        return {k: sum(v for _, v in vs) / len(vs) for k, vs in acc.items()}
 
     fetch, write = load(fetch_dir, "FETCH_SIZE"), load(write_dir, "WRITE_SIZE")
     if "copy_calibration" not in fetch or "copy_calibration" not in write:

@@ -1,0 +1,135 @@
+// Helpers of the MFMA GEMM kernel (nsw_gemm.hip):
+// epilogue / operand-fusion identifiers, the epilogue argument block, the
+// GELU forms, the direct-to-LDS copy, barriers and wait counts, and the LDS
+// row swizzle of the operand stages.
+#pragma once
+
+#include "nsw_common.h"
+
+namespace nsw {
+
+enum Epi {
+  EPI_NONE = NSW_EPI_NONE,
+  EPI_BIAS = NSW_EPI_BIAS,
+  EPI_BIAS_GELU = NSW_EPI_BIAS_GELU,
+  EPI_BIAS_RESIDUAL = NSW_EPI_BIAS_RESIDUAL,
+  EPI_BIAS_GELU_TANH = NSW_EPI_BIAS_GELU_TANH,
+  EPI_SCATTER_RESIDUAL = 11, // bias, row m -> token_of_row(m), + skip[token]
+  EPI_QKV_HN16 = 16,         // bias, then per-head RMSNorm of the q and k
+  EPI_QKV_HN32 = 32,         // columns, for head dims 16 / 32 / 64
+  EPI_QKV_HN64 = 64
+};
+
+// Operand-side fusions (template parameter PRE):
+//   PRE_NONE     y = epi(x . w^T)
+//   PRE_ROWNORM  y = epi(rs . (x . w^T)) with rs[m] = 1/sqrt(mean_k x[m,k]^2 + eps):
+//                the RMSNorm of the rows of x with its weight folded into w
+//                (w[n,k] = W[n,k] * norm_w[k], prepared by the caller), so
+//                that x . w^T * rs = RMSNorm(x) . W^T.  The sums of squares
+//                are accumulated from the x fragments the MFMAs consume
+//                (v_dot2c_f32_bf16 / FMA), rs is applied before the bias.
+//   PRE_ROWNORM_GATHER  as PRE_ROWNORM, and the copy of x row m reads token
+//                row token_of_row(m) of the image (roll by -shift + window
+//                partition folded into the copy addresses).
+//   PRE_ROWSCALE y = epi(rs . (x . w^T)) with rs[m] = 1/sqrt(sum_p P[m,p] / K + eps)
+//                from per-row partial sums of squares P [M, nparts] written by
+//                the producer of x (the proj scatter epilogue): the norm costs
+//                the consumer one read per row instead of a pass over x.
+enum Pre { PRE_NONE = 0, PRE_ROWNORM = 1, PRE_ROWNORM_GATHER = 2, PRE_ROWSCALE = 3 };
+constexpr bool pre_sums_in_loop(int pre) { return pre == PRE_ROWNORM || pre == PRE_ROWNORM_GATHER; }
+
+constexpr int qkv_head_dim(int epi) {
+  return (epi == EPI_QKV_HN16 || epi == EPI_QKV_HN32 || epi == EPI_QKV_HN64) ? epi : 0;
+}
+
+struct EpiArgs {
+  const void* bias;
+  const void* residual;
+  const void* qn_w;
+  const void* kn_w;
+  float eps;
+  int C;       // q/k/v width for the QKV epilogues
+  WinGeom geom;  // EPI_SCATTER_RESIDUAL
+  float* row_sumsq;   // scatter epilogue: optional [tokens, nparts] output; PRE_ROWSCALE: input
+  int nparts;
+};
+
+// GELU with the exact-erf form of nn.GELU(): 0.5 v (1 + erf(v / sqrt 2)).
+// erfc from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7):
+//   erfc(x) = (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-x^2),
+//   t = 1 / (1 + p x), x >= 0.
+// With x = |v| / sqrt 2: 1 + erf(v / sqrt 2) is 2 - erfc(x) for v >= 0 and
+// erfc(x) for v < 0, so GELU(v) = max(v, 0) - |v| erfc(x) / 2 for both signs
+// (no select, no cancellation).  Constants folded: u = |v| sqrt(log2(e) / 2)
+// gives exp(-x^2) = exp2(-u^2) and p x = (p / (sqrt(log2(e)/2) sqrt 2)) u;
+// the polynomial coefficients carry the factor -1/2.  13 VALU instructions,
+// two of them transcendental (v_exp_f32, v_rcp_f32).
+__device__ __forceinline__ float gelu_erf(float v) {
+  const float a = fabsf(v);
+  const float u = a * 0.84932180028801907f;
+  const float e = __builtin_amdgcn_exp2f(-(u * u));
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.27273748087922252f, u, 1.0f));
+  float h = fmaf(-0.5307027145f, t, 0.7265760135f);
+  h = fmaf(h, t, -0.7107068705f);
+  h = fmaf(h, t, 0.142248368f);
+  h = fmaf(h, t, -0.127414796f);
+  h *= t;                                   // -erfc(x) / 2
+  return fmaf(h * e, a, fmaxf(v, 0.0f));
+}
+
+// GELU with the tanh form (nn.GELU(approximate="tanh"), the "gelu" of the
+// reference's Transformer-Engine block): 0.5 v (1 + tanh(u)),
+// u = sqrt(2/pi) (v + 0.044715 v^3).  As 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u)):
+// GELU(v) = v / (1 + exp2(v (c1 + c3 v^2))) with c1 = -2 sqrt(2/pi) log2(e),
+// c3 = 0.044715 c1.  Saturates cleanly: exp2 -> inf gives 0, exp2 -> 0 gives v.
+__device__ __forceinline__ float gelu_tanh(float v) {
+  const float z = v * v;
+  const float a = v * fmaf(-0.10294324f, z, -2.3022082f);
+  return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(a));
+}
+
+// Row blocks per tile group of one XCD (tiles come from xcd_remap).
+constexpr int GROUP_M = 8;
+
+// Buffer resource (V#) over a whole tensor: raw buffer, stride 0, 32-bit
+// byte offsets, num_records = bytes, dword 3 = 0x00020000 (the gfx9 raw
+// buffer format).  Built from wave-uniform values so it lives in SGPRs.
+__device__ __forceinline__ u32x4 make_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = (uint64_t)p;
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// One direct-to-LDS copy: every lane loads 16 bytes at rsrc + voff + soff and
+// the wave's 64 x 16 B land contiguously at LDS byte address lds_addr.
+// Issued as inline asm so that the compiler's wait-count insertion does not
+// see an LDS write in flight (it would otherwise drain all copies before
+// each fragment read); ordering is kept by the explicit vmcnt waits and
+// barriers of the pipeline.  s_nop: M0 write -> LDS-DMA read hazard.
+__device__ __forceinline__ void dma16(const u32x4& rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "m0");
+}
+
+// Barrier between waves with no fence (a fence would wait for every copy)
+// and compiler-level memory ordering on both sides.
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(N) only (expcnt / lgkmcnt fields at their "no wait" maxima).
+#define NSW_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
+// s_waitcnt lgkmcnt(0) only.
+#define NSW_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
+
+// Chunk swizzle of a 128-byte stage row (8 chunks of 16 bytes).
+__device__ __forceinline__ int row_swizzle(int row) {
+  const int r = row & 15;   // position inside the 16-row block
+  return ((r >> 1) & 7) ^ ((r & 1) << 2);
+}
+
+}  // namespace nsw

@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void wsum_partial_kernel(const TP* __restrict_
                                                            const float* __restrict__ clim,
                                                            const TS* __restrict__ std_c,
                                                            const TS* __restrict__ mean_c, int H,
-                                                           int W, int Cch, int rpc, int nchunk,
+                                                           int W, int Cch, int rpc, int nchunk, FastDiv dwq,
                                                            double* __restrict__ partial) {
   const int64_t plane = blockIdx.x / nchunk;
   const int ch = blockIdx.x - (int)(plane * nchunk);
@@ -67,23 +67,44 @@ __global__ __launch_bounds__(256) void wsum_partial_kernel(const TP* __restrict_
     }
   };
   if constexpr (VEC4) {
+    // The band's rows are contiguous in the plane: n4 vectors of 4 from row
+    // h0 on.  Each thread keeps U vector loads of each field in flight (the
+    // loads of a group are issued before its arithmetic); the row of vector
+    // f is f / (W/4) by multiply-shift.
+    constexpr int U = 4;
     const int wq = W >> 2;
-    const int64_t n = (int64_t)(h1 - h0) * wq;
-    for (int64_t i = threadIdx.x; i < n; i += 256) {
-      const int hr = (int)(i / wq);
-      const int x4 = (int)(i - (int64_t)hr * wq);
+    const uint32_t n4 = (uint32_t)(h1 - h0) * (uint32_t)wq;
+    const TP* pb = pp + (int64_t)h0 * W;
+    const float* tb = tp + (int64_t)h0 * W;
+    auto consume = [&](uint32_t f, const float (&p)[4], const f32x4& t) {
+      const int hr = (int)dwq.div(f);
       const int h = h0 + hr;
-      const int64_t off = (int64_t)h * W + 4 * x4;
-      float p[4];
-      load4<TP>(pp + off, p);
-      const f32x4 t = *reinterpret_cast<const f32x4*>(tp + off);
       if constexpr (FULLW) {
+        const int64_t off = (int64_t)h * W + 4 * (int)(f - (uint32_t)hr * (uint32_t)wq);
         acc1(p[0], t[0], wlat[off]); acc1(p[1], t[1], wlat[off + 1]);
         acc1(p[2], t[2], wlat[off + 2]); acc1(p[3], t[3], wlat[off + 3]);
       } else {
         const double w = wlat[h];
         acc1(p[0], t[0], w); acc1(p[1], t[1], w); acc1(p[2], t[2], w); acc1(p[3], t[3], w);
       }
+    };
+    uint32_t i = threadIdx.x;
+    for (; i + (U - 1) * 256 < n4; i += U * 256) {
+      float p[U][4];
+      f32x4 t[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        load4<TP>(pb + 4 * (int64_t)(i + u * 256), p[u]);
+        t[u] = *reinterpret_cast<const f32x4*>(tb + 4 * (int64_t)(i + u * 256));
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) consume(i + u * 256, p[u], t[u]);
+    }
+    for (; i < n4; i += 256) {
+      float p[4];
+      load4<TP>(pb + 4 * (int64_t)i, p);
+      const f32x4 t = *reinterpret_cast<const f32x4*>(tb + 4 * (int64_t)i);
+      consume(i, p, t);
     }
   } else {
     const int64_t n = (int64_t)(h1 - h0) * W;
@@ -144,9 +165,10 @@ static void launch_partial(bool vec4, bool acc, dim3 grid, hipStream_t st, const
                            const float* target, const double* w, const float* clim, const TS* sc,
                            const TS* of, int H, int W, int Cch, int rpc, int nchunk, double* partial) {
   dim3 block(256);
+  const FastDiv dwq = FastDiv::make((uint32_t)(W >= 4 ? W / 4 : 1));
 #define NSW_PARTIAL(V4, AC)                                                                                 \
   hipLaunchKernelGGL((wsum_partial_kernel<TP, TS, V4, AC, FULLW, AFFINE>), grid, block, 0, st, pred, target, \
-                     w, clim, sc, of, H, W, Cch, rpc, nchunk, partial)
+                     w, clim, sc, of, H, W, Cch, rpc, nchunk, dwq, partial)
   if (vec4 && acc) NSW_PARTIAL(true, true);
   else if (vec4) NSW_PARTIAL(true, false);
   else if (acc) NSW_PARTIAL(false, true);
