@@ -1,7 +1,14 @@
 // Window attention core: o = softmax(q k^T * scale + mask) v per (window, head)
 // (the F.scaled_dot_product_attention call of models/swin_helpers.py:247).
 //
-// bf16 path (attn_mfma_kernel): one 256-thread workgroup per (window, head).
+// bf16, head dim 64, 9 x 18 windows, shift mask from indices or none
+// (attn_dma_kernel, the model's case): K and V rows are copied straight into
+// LDS and V^T fragments come from transposing LDS reads (see below the
+// direct-to-LDS section); the per-block arithmetic is that of
+// attn_mfma_kernel, in the same order, so the two give identical bits.
+//
+// bf16 path (attn_mfma_kernel, other head dims and window sizes, mask
+// tensors): one 256-thread workgroup per (window, head).
 // K [keys x hd] and V^T [hd x keys] of the window are staged in LDS (zero
 // padded to a multiple of 32 keys).  Each wavefront takes 16-query blocks and
 //   1. computes S^T = K Q^T with v_mfma_f32_16x16x32_bf16, so that lane l
@@ -276,7 +283,7 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
     // v_permlane16_swap of (db = 2j, db = 2j+1) pairs lane groups fg = 2m and
     // 2m+1: afterwards the even group holds dims 16 db + 8m .. +7 of db = 2j
     // and the odd group those of db = 2j+1, so every lane writes 16 B chunks.
-    const float inv = 1.0f / Z[0];
+    const float inv = __builtin_amdgcn_rcpf(Z[0]);
     float lo[NDB / 2][2], hi[NDB / 2][2];
 #pragma unroll
     for (int j = 0; j < NDB / 2; ++j) {
@@ -298,6 +305,244 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
       for (int j = 0; j < NDB / 2; ++j)
         *reinterpret_cast<f32x4*>(orow + 32 * j) = f32x4{lo[j][0], lo[j][1], hi[j][0], hi[j][1]};
     }
+  }
+}
+
+// ------------------------------------------- bf16 MFMA, direct-to-LDS ----
+// K and V rows of a (window, head) item are copied straight into LDS with
+// buffer_load ... lds, row-major (128 B per row for head dim 64), their
+// 16-byte chunks XOR-swizzled by row (sw_chunk; conflict-free fragment
+// reads, as k_chunk).  The PV product reads its V^T fragments with
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4
+// of the 4-element vectors addressed by lanes i/4, 4 + i/4, 8 + i/4 and
+// 12 + i/4, so lanes addressing rows 4g + i/4 at dims 16 db + 4 (i%4) yield
+// column 16 db + i of rows 4g .. 4g+3; two such reads per 16-dim block give
+// keys {4g+r, 16+4g+r}, the key order of the probability registers.
+__device__ __forceinline__ int sw_chunk(int row, int ch) {
+  return ch ^ (((row >> 1) & 7) ^ ((row & 1) << 2));
+}
+
+// The resource built from kernel arguments, pinned to SGPRs (the inline asm
+// operands below require scalar registers).
+__device__ __forceinline__ u32x4 uniform_rsrc(const void* p, uint32_t bytes) {
+  const u32x4 r = make_rsrc(p, bytes);
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((int)r[0]), (uint32_t)__builtin_amdgcn_readfirstlane((int)r[1]),
+               (uint32_t)__builtin_amdgcn_readfirstlane((int)r[2]), (uint32_t)__builtin_amdgcn_readfirstlane((int)r[3])};
+}
+
+// 16-byte store from inline asm.  A VALU write to the data VGPRs of a 16-byte
+// store needs 2 wait states after the store on gfx950; the compiler cannot
+// see the store inside the asm, so the s_nop provides them.
+__device__ __forceinline__ void store16_asm(const u32x4& rsrc, uint32_t voff, const f32x4& v) {
+  asm volatile("buffer_store_dwordx4 %0, %1, %2, 0 offen\n\ts_nop 1" : : "v"(v), "v"(voff), "s"(rsrc) : "memory");
+}
+
+// One 16-query block of a (window, head) item with head dim 64: K rows and V
+// rows (KP of each, 128 B per row, 16-byte chunks placed by sw_chunk) in LDS,
+// V rows past L zero (so that their zero probabilities give exact zeros), the
+// block's Q fragments in registers.  Computes S^T = K Q^T, the masked
+// softmax in the exp2 domain (row max by permlane reduction, row sums by an
+// MFMA against a ones block), O^T = V^T P^T with V^T fragments from
+// ds_read_b64_tr_b16, and stores the block's rows of o (NDB / 2 16-byte
+// stores per lane, issued from inline asm; queries past L go to offset
+// obytes, past the end of o, where they are dropped).
+template <int NKB>
+__device__ __forceinline__ void attn_qblock64(const AttnArgs& a, const char* Ks, const char* Vs, const bf16x8 (&qf)[2],
+                                              int q, int win, int head, bool shifted, const uint64_t* cls,
+                                              const u32x4& ro, uint32_t obytes, int fr, int fg) {
+  constexpr int HD = 64;
+  constexpr int KP = ((NKB * 16 + 31) / 32) * 32;
+  constexpr int NS = HD / 32, NDB = HD / 16, NKS = KP / 32;
+  constexpr float LOG2E = 1.4426950408889634f;
+  typedef short i16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) i16x4 lds_s4;
+  const int L = a.L, C = a.C;
+  const int qc = q < L ? q : L - 1;
+  const float zscale = a.scale * LOG2E;
+  const float smask = -100.0f / a.scale;
+  const bf16x8 ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+  // S^T = K Q^T, K fragments KD blocks ahead
+  constexpr int KD = NKB < 4 ? NKB : 4;
+  f32x4 S[NKB];
+  bf16x8 kf[KD][NS];
+#pragma unroll
+  for (int kb = 0; kb < KD; ++kb)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int r = kb * 16 + fr;
+      kf[kb][s] = *reinterpret_cast<const bf16x8*>(Ks + r * 128 + sw_chunk(r, 4 * s + fg) * 16);
+    }
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) S[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kb % KD][s], qf[s], S[kb], 0, 0, 0);
+    if (kb + KD < NKB) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int r = (kb + KD) * 16 + fr;
+        kf[kb % KD][s] = *reinterpret_cast<const bf16x8*>(Ks + r * 128 + sw_chunk(r, 4 * s + fg) * 16);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // lane: query fr, keys 16 kb + 4 fg + r
+  if (shifted) {
+    const int qcls = (int)((cls[qc >> 6] >> (qc & 63)) & 1);
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const unsigned bits = (unsigned)(cls[kb >> 2] >> (16 * (kb & 3) + 4 * fg)) & 0xFu;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if ((int)((bits >> r) & 1u) != qcls) S[kb][r] += smask;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if ((NKB - 1) * 16 + 4 * fg + r >= L) S[NKB - 1][r] = -INFINITY;
+  float mx = S[0][0];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[kb][r]);
+  mx = rows4_max(mx);
+  const float off = -mx * zscale;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) S[kb][r] = __builtin_amdgcn_exp2f(fmaf(S[kb][r], zscale, off));
+
+  // O^T = V^T P^T: V^T fragments of 32-key step ks from two transposed
+  // reads (keys 32ks + 4fg + 0..3 and 32ks + 16 + 4fg + 0..3, dim 16db + fr)
+  f32x4 O[NDB], Z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) O[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 vf[2][NDB];
+  auto load_v = [&](int b, int ks) {
+    const int r0 = 32 * ks + 4 * fg + fr / 4;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const int lc = 2 * db + (fr & 3) / 2;
+      const int half = (fr & 1) * 8;
+      const i16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s4*)(Vs + r0 * 128 + sw_chunk(r0, lc) * 16 + half));
+      const i16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s4*)(Vs + (r0 + 16) * 128 + sw_chunk(r0 + 16, lc) * 16 + half));
+      const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo4), h4 = __builtin_bit_cast(bf16x4, hi4);
+      vf[b][db] = bf16x8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+    }
+  };
+  load_v(0, 0);
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    if (ks + 1 < NKS) load_v((ks + 1) & 1, ks + 1);
+    bf16x8 pf;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pf[r] = (bf16)S[2 * ks][r];
+      pf[4 + r] = (2 * ks + 1 < NKB) ? (bf16)S[2 * ks + 1][r] : (bf16)0.f;
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[ks & 1][db], pf, O[db], 0, 0, 0);
+    Z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, Z, 0, 0, 0);
+  }
+  // 16-byte stores after pairing head-dim blocks (as attn_mfma_kernel);
+  // queries past L (and whole padding blocks) go to an offset past the
+  // end of o, where the store is dropped
+  const float inv = __builtin_amdgcn_rcpf(Z[0]);
+  const uint32_t obase = (((uint32_t)win * (uint32_t)L + (uint32_t)q) * (uint32_t)C +
+                          (uint32_t)(head * HD + 8 * (fg >> 1) + 16 * (fg & 1))) * 2u;
+#pragma unroll
+  for (int j = 0; j < NDB / 2; ++j) {
+    const bf16x4 e = {(bf16)(O[2 * j][0] * inv), (bf16)(O[2 * j][1] * inv), (bf16)(O[2 * j][2] * inv),
+                      (bf16)(O[2 * j][3] * inv)};
+    const bf16x4 f = {(bf16)(O[2 * j + 1][0] * inv), (bf16)(O[2 * j + 1][1] * inv),
+                      (bf16)(O[2 * j + 1][2] * inv), (bf16)(O[2 * j + 1][3] * inv)};
+    const f32x2 ev = __builtin_bit_cast(f32x2, e), fv = __builtin_bit_cast(f32x2, f);
+    float l0 = ev[0], l1 = ev[1], h0 = fv[0], h1 = fv[1];
+    permlane16_swap(l0, h0);
+    permlane16_swap(l1, h1);
+    store16_asm(ro, q < L ? obase + 64u * j : obytes, f32x4{l0, l1, h0, h1});
+  }
+}
+
+// One workgroup per (window, head) item, head dim 64, shift mask from indices
+// or none (three workgroups per CU).  K and V rows go straight to LDS with
+// buffer_load ... lds (row-major, chunks placed by sw_chunk: no VGPR staging,
+// no transposing LDS writes); each wave's Q fragments are loaded into
+// registers alongside.  Waves take query blocks wave, wave + 4, ...
+template <int NKB>
+__global__ __launch_bounds__(256, 3) void attn_dma_kernel(AttnArgs a, int nitems) {
+  constexpr int HD = 64;
+  constexpr int KP = ((NKB * 16 + 31) / 32) * 32;
+  constexpr int PART = KP * 128;
+  constexpr int RG = KP / 8;
+  static_assert((2 * RG) % 4 == 0, "copies split evenly over 4 waves");
+  constexpr int NDMA = 2 * RG / 4;
+  constexpr int QPW = (NKB + 3) / 4;
+  constexpr int NS = HD / 32, NCLS = (KP + 63) / 64;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * PART];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, fg = lane >> 4;
+  const int L = a.L, C = a.C;
+  const uint32_t ld = 3u * (uint32_t)C;
+  const int item = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int win = item / a.heads, head = item - win * a.heads;
+  const uint32_t qkv_bytes = (uint32_t)((uint64_t)nitems / a.heads * L * ld * 2u);
+  const u32x4 rq = uniform_rsrc(a.qkv, qkv_bytes);
+  const uint32_t obytes = (uint32_t)((uint64_t)nitems / a.heads * L * (uint32_t)C * 2u);
+  const u32x4 ro = uniform_rsrc(a.o, obytes);
+
+  // Q fragments of this wave's query blocks (rows past L re-read row L - 1)
+  const bf16* base = (const bf16*)a.qkv + (int64_t)win * L * ld + head * HD;
+  bf16x8 qf[QPW][NS];
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int q = (wave + 4 * i) * 16 + fr;
+    const int qc = q < L ? q : L - 1;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[i][s] = *reinterpret_cast<const bf16x8*>(base + qc * ld + 32 * s + 8 * fg);
+  }
+  // K rows to [0, PART), V rows to [PART, 2 PART): copy j of this wave is
+  // 8-row group d = wave * NDMA + j
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  const uint32_t soff = ((uint32_t)win * (uint32_t)L * ld + (uint32_t)head * HD) * 2u;
+#pragma unroll
+  for (int j = 0; j < NDMA; ++j) {
+    const int d = wave * NDMA + j;
+    const int part = d / RG, rg = d - part * RG;
+    const int row = rg * 8 + lane / 8;
+    const int lc = sw_chunk(row, lane % 8);
+    // V rows past L read from offset qkv_bytes, past the end of qkv: the
+    // range check returns zeros, which land in LDS as the padding rows
+    const uint32_t voff = part == 1 && row >= L
+                              ? qkv_bytes
+                              : ((uint32_t)row * ld + (uint32_t)(part + 1) * (uint32_t)C) * 2u + (uint32_t)lc * 16u;
+    dma16(rq, sbase + (uint32_t)(part * PART + rg * 1024), voff, soff);
+  }
+
+  const bool shifted = window_in_last_band(a, win);
+  uint64_t cls[NCLS];
+  {
+    const int thr = shifted ? (a.g.ws0 - a.g.s0) * a.g.ws1 : 0;
+    const int wa = shifted ? a.g.wa : 1;
+#pragma unroll
+    for (int w = 0; w < NCLS; ++w) {
+      const int key = 64 * w + lane;
+      cls[w] = __ballot(shifted && key < L && (key % wa) >= thr);
+    }
+  }
+  NSW_WAIT_VMCNT(0);
+  wg_barrier();
+
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int qb = wave + 4 * i;
+    if (qb >= NKB) break;
+    attn_qblock64<NKB>(a, smem, smem + PART, qf[i], qb * 16 + fr, win, head, shifted, cls, ro, obytes, fr, fg);
   }
 }
 
@@ -389,6 +634,20 @@ static int launch_mfma(const AttnArgs& a, int64_t grid, hipStream_t st) {
   return launch_mfma_seq<HD>(a, grid, st, std::make_integer_sequence<int, 24>{});
 }
 
+// Head dim 64 without a mask tensor, 9 x 18 windows (11 key blocks):
+// attn_dma_kernel.  Returns -1 when it does not apply: the 32-bit byte
+// offsets of the copies (qkv_bytes, the drop offset of the padding rows, plus
+// the item's offset) must stay below 2^32, and the tensors must be 16-byte
+// aligned.
+static int launch_dma(const AttnArgs& a, int64_t items, hipStream_t st) {
+  const int nkb = (a.L + 15) / 16;
+  const uint64_t qkv_bytes = (uint64_t)items / a.heads * a.L * 3ull * a.C * 2ull;
+  if (nkb != 11 || qkv_bytes >= (1ull << 31) || items >= (1ll << 31) || items % a.heads != 0) return -1;
+  if ((uintptr_t)a.qkv % 16 != 0 || (uintptr_t)a.o % 16 != 0) return -1;
+  hipLaunchKernelGGL((attn_dma_kernel<11>), dim3((unsigned)items), dim3(256), 0, st, a, (int)items);
+  return 0;
+}
+
 template <typename T>
 static int launch_scalar(const AttnArgs& a, int hd, int64_t grid, hipStream_t st) {
   switch (hd) {
@@ -438,8 +697,11 @@ extern "C" int nsw_window_attention(const void* qkv, void* o, const float* mask,
   const int64_t grid = Bw * num_heads;
   if (dtype == NSW_DTYPE_BF16) {
     int rc = -1;
-    if (hd == 64) rc = launch_mfma<64>(a, grid, st);
-    else if (hd == 32) rc = launch_mfma<32>(a, grid, st);
+    if (hd == 64 && a.mask_mode != MASK_TENSOR) rc = launch_dma(a, grid, st);
+    if (rc != 0) {
+      if (hd == 64) rc = launch_mfma<64>(a, grid, st);
+      else if (hd == 32) rc = launch_mfma<32>(a, grid, st);
+    }
     if (rc != 0) rc = launch_scalar<bf16>(a, hd, grid, st);
     if (rc != 0) return set_error(NSW_ERR_UNSUPPORTED, "%s: head_dim=%d, L=%lld unsupported", what, hd, (long long)L);
   } else if (dtype == NSW_DTYPE_F32) {

@@ -148,6 +148,43 @@ __device__ __forceinline__ float rows4_max(float x) {
   return fmaxf(c, d);
 }
 
+// ------------------------------------------- direct-to-LDS copies, waits ----
+// Buffer resource (V#) over a whole tensor: raw buffer, stride 0, 32-bit
+// byte offsets, num_records = bytes, dword 3 = 0x00020000 (the gfx9 raw
+// buffer format).  Built from wave-uniform values so it lives in SGPRs.
+__device__ __forceinline__ u32x4 make_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t a = (uint64_t)p;
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// One direct-to-LDS copy: every lane loads 16 bytes at rsrc + voff + soff and
+// the wave's 64 x 16 B land contiguously at LDS byte address lds_addr.
+// Issued as inline asm so that the compiler's wait-count insertion does not
+// see an LDS write in flight (it would otherwise drain all copies before
+// each fragment read); ordering is kept by the explicit vmcnt waits and
+// barriers of the pipeline.  s_nop: M0 write -> LDS-DMA read hazard.
+__device__ __forceinline__ void dma16(const u32x4& rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "m0");
+}
+
+// Barrier between waves with no fence (a fence would wait for every copy)
+// and compiler-level memory ordering on both sides.
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(N) only (expcnt / lgkmcnt fields at their "no wait" maxima).
+#define NSW_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
+// s_waitcnt lgkmcnt(0) only.
+#define NSW_WAIT_LGKMCNT0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
+
+
 // ------------------------------------------------------- XCD placement ----
 // Workgroups are dispatched round-robin over the 8 XCDs (XCD x receives ids
 // x, x+8, x+16, ...), each with its own L2.  This bijection over [0, n) gives

@@ -150,6 +150,8 @@ ATTN_CASES = [
     (1, 1, 18, 36, 128, 2, (9, 18), (0, 0)),
     (2, 2, 18, 36, 128, 2, (9, 18), (4, 9)),
     (1, 1, 16, 32, 64, 2, (4, 8), (2, 4)),
+    (1, 1, 9, 18, 128, 2, (9, 18), (0, 0)),
+    (3, 1, 18, 36, 320, 5, (9, 18), (4, 9)),
 ]
 
 
@@ -175,6 +177,45 @@ def test_window_attention(device, dtype, B, T, H, W, C, heads, ws, shift, mode):
         got = ops.window_attention(qkv.to(device), heads, scale, mask=mask.to(device))
     want = attention_oracle(qkv, heads, scale, mask)
     assert rel_l2(got, want) < TOL[dtype]
+
+
+@pytest.mark.parametrize("H,W,C,heads", [(180, 360, 1024, 16), (9, 18, 128, 2), (18, 36, 320, 5)])
+def test_window_attention_kernels_agree(device, H, W, C, heads):
+    """bf16, head dim 64, 9 x 18 windows: the persistent kernel (index mode,
+    no mask) and the staged one (an all-zero mask tensor) do the same
+    arithmetic in the same order, so their outputs are bit-identical."""
+    from nsw import ops
+    ws = (9, 18)
+    L = ws[0] * ws[1]
+    nW = (H // ws[0]) * (W // ws[1])
+    g = torch.Generator().manual_seed(13)
+    qkv = (torch.randn(nW, L, 3 * C, generator=g) * 2).to(torch.bfloat16).to(device)
+    scale = (C // heads) ** -0.5
+    a = ops.window_attention(qkv, heads, scale, geometry=(H, W, ws, (0, 0), 1))
+    b = ops.window_attention(qkv, heads, scale, mask=torch.zeros(nW, L, L, device=device))
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("shift", [(0, 0), (4, 9)])
+def test_window_attention_windows_isolated(device, shift):
+    """bf16, head dim 64: a window's output depends on its own rows only.
+    Every third window holds NaN; the others (including the last, whose
+    padding rows lie past the end of qkv) must match the oracle.  512 windows
+    x 2 heads, so that each CU runs several items and reuses its LDS after
+    NaN windows."""
+    from nsw import ops
+    H, W, C, heads, ws = 144, 576, 128, 2, (9, 18)
+    L = ws[0] * ws[1]
+    nW = (H // ws[0]) * (W // ws[1])
+    g = torch.Generator().manual_seed(14)
+    qkv = torch.randn(nW, L, 3 * C, generator=g).to(torch.bfloat16)
+    bad = torch.arange(nW) % 3 == 1
+    qkv[bad] = float("nan")
+    scale = (C // heads) ** -0.5
+    got = ops.window_attention(qkv.to(device), heads, scale, geometry=(H, W, ws, shift, 1)).cpu()
+    want = attention_oracle(qkv, heads, scale, ref.make_attention_mask(H, W, ws, shift, 1))
+    assert torch.isfinite(got[~bad]).all()
+    assert rel_l2(got[~bad], want[~bad]) < TOL[torch.bfloat16]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
