@@ -322,7 +322,7 @@ TRACE_NAMES = [
     ("_ZN3nsw11gemm_kernelIDF16bLi3ELi0E", "fc2"),
     ("_ZN3nsw11gemm_kernelIDF16bLi64ELi0E", "qkv"),
     ("_ZN3nsw11gemm_kernelIDF16bLi11ELi0E", "proj_scatter_sumsq"),
-    ("attn_persist_kernel", "attention"),
+    ("attn_dma_kernel", "attention"),
     ("attn_mfma_kernel", "attention"),
     ("row_map_kernel", "gather_norm1"),
     ("wsum_partial_kernel", "metrics_unnorm"),

@@ -146,13 +146,13 @@ int nsw_proj_reverse_residual(const void* o, const void* wproj, const void* bpro
                               int64_t s1, int dtype, void* stream);
 
 /* Number of partial sums per row that nsw_proj_reverse_residual_sumsq writes
- * for rows of C elements: one per 256 bytes of row, ceil(C * esize / 256). */
+ * for rows of C elements: one per 512 bytes of row, ceil(C * esize / 512). */
 int64_t nsw_row_sumsq_parts(int64_t C, int dtype);
 
 /* nsw_proj_reverse_residual that also writes, for each output row (token t),
  * partial sums of the squares of the values it stores (after the residual,
  * in the output dtype): row_sumsq[t * P + p] = sum of y[t, c]^2 over the p-th
- * 256-byte segment of the row, P = nsw_row_sumsq_parts(C, dtype), fp32.
+ * 512-byte segment of the row, P = nsw_row_sumsq_parts(C, dtype), fp32.
  * These are the statistics of Block.forward's norm2 (models/swin_helpers.py
  * :457, nn.RMSNorm over h1), so that the consumer GEMM (nsw_linear_rowscale)
  * normalises h1 without a separate pass over it. */

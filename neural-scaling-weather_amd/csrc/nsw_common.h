@@ -163,10 +163,20 @@ __device__ __forceinline__ u32x4 make_rsrc(const void* p, uint32_t bytes) {
 // see an LDS write in flight (it would otherwise drain all copies before
 // each fragment read); ordering is kept by the explicit vmcnt waits and
 // barriers of the pipeline.  s_nop: M0 write -> LDS-DMA read hazard.
+// The scalar operands pass through v_readfirstlane, which the compiler drops
+// when they already live in SGPRs: a wave-uniform value computed along paths
+// the divergence analysis cannot prove uniform would otherwise reach the
+// "s" constraints in a VGPR (an assembler error).
 __device__ __forceinline__ void dma16(const u32x4& rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  const u32x4 r = {(uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[0]),
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[1]),
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[2]),
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[3])};
+  const uint32_t l = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr);
+  const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)soff);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+               : "s"(l), "v"(voff), "s"(r), "s"(so)
                : "m0");
 }
 

@@ -534,12 +534,14 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
           if (ok) *reinterpret_cast<u32x4*>(Y + (int64_t)orow[cur][b] * N + n) = ov[b];
         }
         if constexpr (SCAT) {
-          // partial sum of squares over the 16 lanes (16 * VEC columns) of a
-          // DPP row, one float per 256 bytes of output row
+          // partial sum of squares over 32 lanes (32 * VEC columns: two DPP
+          // rows, even row first), one float per 512 bytes of output row
           if (ea.row_sumsq != nullptr) {
-            ssq = row16_sum(ssq);
-            if ((lane & 15) == 0 && ok)
-              ea.row_sumsq[(int64_t)orow[cur][b] * ea.nparts + n / (16 * VEC)] = ssq;
+            float lo16 = row16_sum(ssq), hi16 = lo16;
+            permlane16_swap(lo16, hi16);
+            ssq = lo16 + hi16;
+            if ((lane & 31) == 0 && ok)
+              ea.row_sumsq[(int64_t)orow[cur][b] * ea.nparts + n / (32 * VEC)] = ssq;
           }
         }
       }
@@ -596,11 +598,11 @@ int gemm_qkv(const void* x, const void* wqkv, const void* bqkv, const void* qn_w
   return dispatch_gemm<EPI_QKV_HN16>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
 }
 
-// Partial sums of squares per output row: one float per 256 bytes of row
-// (16 lanes of 16-byte stores in the scatter epilogue).
+// Partial sums of squares per output row: one float per 512 bytes of row
+// (32 lanes of 16-byte stores in the scatter epilogue).
 int64_t sumsq_parts(int64_t C, int dtype) {
   const int64_t es = dtype == NSW_DTYPE_F32 ? 4 : 2;
-  return (C * es + 255) / 256;
+  return (C * es + 511) / 512;
 }
 
 int gemm_proj_scatter(const void* o, const void* wproj, const void* bproj, const void* skip, void* y,

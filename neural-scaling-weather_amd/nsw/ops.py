@@ -323,7 +323,7 @@ def proj_reverse_residual(o: torch.Tensor, wproj: torch.Tensor, bproj: torch.Ten
 def proj_reverse_residual_sumsq(o: torch.Tensor, wproj: torch.Tensor, bproj: torch.Tensor, skip: torch.Tensor,
                                 window_size, shift_size):
     """proj_reverse_residual that also returns the partial sums of squares of
-    each output row [B*T*H*W, P] (fp32, one per 256 bytes of row), the
+    each output row [B*T*H*W, P] (fp32, one per 512 bytes of row), the
     statistics of the RMSNorm that follows."""
     B, T, H, W, C = skip.shape
     dev = _dev(o, wproj, bproj, skip)

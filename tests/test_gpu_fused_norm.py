@@ -135,10 +135,10 @@ def test_proj_reverse_residual_sumsq(device, dtype, B, T, H, W, C, ws, shift):
     y, ss = ops.proj_reverse_residual_sumsq(d(o), d(wp), d(bp), d(skip), ws, shift)
     assert torch.equal(y, y0)
     es = 2 if dtype == torch.bfloat16 else 4
-    P = (C * es + 255) // 256
+    P = (C * es + 511) // 512
     assert ss.shape == (B * T * H * W, P) and ss.dtype == torch.float32
     assert _lib.lib().nsw_row_sumsq_parts(C, ops.dtype_code(y)) == P
-    want = segment_sumsq(y.reshape(-1, C), 256 // es)
+    want = segment_sumsq(y.reshape(-1, C), 512 // es)
     assert rel_l2(ss, want) < 1e-6
     assert (ss.double().cpu() - want).abs().max().item() <= 1e-5 * want.abs().max().item()
 
@@ -158,7 +158,7 @@ def test_linear_rowscale(device, dtype, M, N, K, epi):
     r = torch.randn(M, N, generator=g).to(dtype)
     eps = torch.finfo(dtype).eps
     es = 2 if dtype == torch.bfloat16 else 4
-    ss = segment_sumsq(x.float(), 256 // es).float().contiguous()
+    ss = segment_sumsq(x.float(), 512 // es).float().contiguous()
     code = {"none": _lib.NSW_EPI_NONE, "gelu": _lib.NSW_EPI_BIAS_GELU, "residual": _lib.NSW_EPI_BIAS_RESIDUAL}[epi]
     d = lambda t: t.to(device)
     got = ops.linear_rowscale(d(x), d(fold(w, nw, dtype)), d(ss), None if epi == "none" else d(b),

@@ -52,9 +52,9 @@ def test_workspace_sizes_are_host_only(L):
     s = _lib.BlockShape(1, 1, 180, 360, 1024, 16, 9, 18, 4, 9, 4096, 1e-7, _lib.NSW_DTYPE_BF16)
     M = 180 * 360
     n = L.nsw_block_workspace_size(s)
-    parts = 1024 * 2 // 256                      # row sums of squares: one float per 256 B of h1 row
+    parts = 1024 * 2 // 512                      # row sums of squares: one float per 512 B of h1 row
     assert L.nsw_row_sumsq_parts(1024, _lib.NSW_DTYPE_BF16) == parts
-    assert L.nsw_row_sumsq_parts(1024, _lib.NSW_DTYPE_F32) == 16
+    assert L.nsw_row_sumsq_parts(1024, _lib.NSW_DTYPE_F32) == 8
     assert n >= M * (1024 + 4096 + 1024) * 2 + M * parts * 4
     assert n < M * (1024 + 4096 + 1024) * 2 + M * parts * 4 + 4096
     assert L.nsw_weighted_metrics_workspace_size(70, 720, 1440) > 0
