@@ -546,6 +546,165 @@ __global__ __launch_bounds__(256, 3) void attn_dma_kernel(AttnArgs a, int nitems
   }
 }
 
+// ---------------------------------------------------------- fp32 MFMA ----
+// fp32 (the reference's inference precision), head dim 64, 9 x 18 windows,
+// shift mask from indices or none: one 512-thread workgroup per (window,
+// head).  K and V rows (256 B of fp32) are copied straight into LDS with
+// their 16-byte chunks XOR-swizzled by row: K chunk c of row r at
+// c ^ (r & 15) (a fragment read, 16 rows x one chunk, covers every bank), V
+// chunk c at c ^ (((r >> 2) & 3) << 2) (the rows 16kb + 4g + r' that lane
+// groups g read in one PV step fall in different 64-byte bank groups).  With
+// v_mfma_f32_16x16x4_f32:
+//   S^T = K Q^T: four MFMAs per 16-byte K fragment (instruction e takes head
+//     dims 16s + 4g + e from lane group g), so lane (i, g) holds the logits of
+//     query i for keys 16kb + 4g + r as in the bf16 kernels, and the mask and
+//     exp2-domain softmax are theirs (probabilities stay fp32);
+//   O^T = V^T P^T: for key step (kb, r) lane (i, g) supplies V[16kb + 4g + r]
+//     [16db + i] (A) and its own probability for key 16kb + 4g + r (B);
+//   row sums of P on the VALU (lane sums, then across the four lane groups).
+// Lane (i, g) ends with O[query i][16db + 4g .. +3]: one 16-byte store per
+// dim block.  The eight waves (two per SIMD) take query blocks w and w + 8.
+// Key rows past L are zero-filled by the copies' range check (V) or masked to
+// -inf (K).
+template <int NKB>
+__global__ __launch_bounds__(512, 1) void attn_f32_kernel(AttnArgs a, int nitems) {
+  constexpr int HD = 64;
+  constexpr int KR = NKB * 16;                  // rows of K and of V in LDS
+  constexpr int PART = KR * HD * 4;
+  constexpr int NW = 8;
+  constexpr int RG = KR / 4;                    // 4-row copies per part
+  static_assert((2 * RG) % NW == 0, "copies split evenly over the waves");
+  constexpr int NDMA = 2 * RG / NW;
+  constexpr int QPW = (NKB + NW - 1) / NW;
+  constexpr int NS = HD / 16, NDB = HD / 16, NCLS = (KR + 63) / 64;
+  constexpr float LOG2E = 1.4426950408889634f;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * PART];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int fr = lane & 15, fg = lane >> 4;
+  const int L = a.L, C = a.C;
+  const uint32_t ld = 3u * (uint32_t)C;
+  const int item = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const int win = item / a.heads, head = item - win * a.heads;
+  const uint32_t qkv_bytes = (uint32_t)((uint64_t)nitems / a.heads * L * ld * 4u);
+  const u32x4 rq = uniform_rsrc(a.qkv, qkv_bytes);
+
+  // K rows to [0, PART), V rows to [PART, 2 PART)
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  const uint32_t soff = ((uint32_t)win * (uint32_t)L * ld + (uint32_t)head * HD) * 4u;
+#pragma unroll
+  for (int j = 0; j < NDMA; ++j) {
+    const int d = wave * NDMA + j;
+    const int part = d / RG, rg = d - part * RG;
+    const int row = rg * 4 + lane / 16;
+    const int sw = part == 0 ? (row & 15) : (((row >> 2) & 3) << 2);
+    const int c = (lane % 16) ^ sw;
+    const uint32_t voff = part == 1 && row >= L
+                              ? qkv_bytes
+                              : ((uint32_t)row * ld + (uint32_t)(part + 1) * (uint32_t)C) * 4u + (uint32_t)c * 16u;
+    dma16(rq, sbase + (uint32_t)(part * PART + rg * 1024), voff, soff);
+  }
+
+  const bool shifted = window_in_last_band(a, win);
+  uint64_t cls[NCLS];
+  {
+    const int thr = shifted ? (a.g.ws0 - a.g.s0) * a.g.ws1 : 0;
+    const int wa = shifted ? a.g.wa : 1;
+#pragma unroll
+    for (int w = 0; w < NCLS; ++w) {
+      const int key = 64 * w + lane;
+      cls[w] = __ballot(shifted && key < L && (key % wa) >= thr);
+    }
+  }
+  NSW_WAIT_VMCNT(0);
+  wg_barrier();
+
+  const float* base = (const float*)a.qkv + (int64_t)win * L * ld + head * HD;
+  const char* Ks = smem;
+  const char* Vs = smem + PART;
+  const float zscale = a.scale * LOG2E;
+  const float smask = -100.0f / a.scale;
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int qb = wave + NW * i;
+    if (qb >= NKB) break;
+    const int q = qb * 16 + fr;
+    const int qc = q < L ? q : L - 1;
+    f32x4 qf[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[s] = *reinterpret_cast<const f32x4*>(base + (int64_t)qc * ld + 16 * s + 4 * fg);
+    // S^T = K Q^T
+    f32x4 S[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      S[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int r = kb * 16 + fr;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const f32x4 kf = *reinterpret_cast<const f32x4*>(Ks + r * (HD * 4) + (((4 * s + fg) ^ (r & 15)) * 16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[e], qf[s][e], S[kb], 0, 0, 0);
+      }
+    }
+    // lane: query fr, keys 16 kb + 4 fg + r
+    if (shifted) {
+      const int qcls = (int)((cls[qc >> 6] >> (qc & 63)) & 1);
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const unsigned bits = (unsigned)(cls[kb >> 2] >> (16 * (kb & 3) + 4 * fg)) & 0xFu;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if ((int)((bits >> r) & 1u) != qcls) S[kb][r] += smask;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if ((NKB - 1) * 16 + 4 * fg + r >= L) S[NKB - 1][r] = -INFINITY;
+    float mx = S[0][0];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, S[kb][r]);
+    mx = rows4_max(mx);
+    const float off = -mx * zscale;
+    float zl = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        S[kb][r] = __builtin_amdgcn_exp2f(fmaf(S[kb][r], zscale, off));
+        zl += S[kb][r];
+      }
+    const float z = rows4_sum(zl);
+    // O^T = V^T P^T
+    f32x4 O[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) O[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = kb * 16 + 4 * fg + r;
+        const char* vr = Vs + row * (HD * 4) + (fr & 3) * 4;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const float v = *reinterpret_cast<const float*>(vr + (((4 * db + fr / 4) ^ (fg << 2)) * 16));
+          O[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(v, S[kb][r], O[db], 0, 0, 0);
+        }
+      }
+    if (q < L) {
+      const float inv = 1.0f / z;
+      float* orow = (float*)a.o + ((int64_t)win * L + q) * (int64_t)C + head * HD + 4 * fg;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        *reinterpret_cast<f32x4*>(orow + 16 * db) =
+            f32x4{O[db][0] * inv, O[db][1] * inv, O[db][2] * inv, O[db][3] * inv};
+    }
+  }
+}
+
 // ------------------------------------------------------- generic (fp32) ----
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void attn_scalar_kernel(AttnArgs a) {
@@ -648,6 +807,17 @@ static int launch_dma(const AttnArgs& a, int64_t items, hipStream_t st) {
   return 0;
 }
 
+// fp32, head dim 64 without a mask tensor, 9 x 18 windows: attn_f32_kernel
+// (conditions as launch_dma, with 4-byte elements).
+static int launch_f32(const AttnArgs& a, int64_t items, hipStream_t st) {
+  const int nkb = (a.L + 15) / 16;
+  const uint64_t qkv_bytes = (uint64_t)items / a.heads * a.L * 3ull * a.C * 4ull;
+  if (nkb != 11 || qkv_bytes >= (1ull << 31) || items >= (1ll << 31) || items % a.heads != 0) return -1;
+  if ((uintptr_t)a.qkv % 16 != 0 || (uintptr_t)a.o % 16 != 0) return -1;
+  hipLaunchKernelGGL((attn_f32_kernel<11>), dim3((unsigned)items), dim3(512), 0, st, a, (int)items);
+  return 0;
+}
+
 template <typename T>
 static int launch_scalar(const AttnArgs& a, int hd, int64_t grid, hipStream_t st) {
   switch (hd) {
@@ -705,6 +875,7 @@ extern "C" int nsw_window_attention(const void* qkv, void* o, const float* mask,
     if (rc != 0) rc = launch_scalar<bf16>(a, hd, grid, st);
     if (rc != 0) return set_error(NSW_ERR_UNSUPPORTED, "%s: head_dim=%d, L=%lld unsupported", what, hd, (long long)L);
   } else if (dtype == NSW_DTYPE_F32) {
+    if (hd == 64 && a.mask_mode != MASK_TENSOR && launch_f32(a, grid, st) == 0) return check_launch(what);
     if (launch_scalar<float>(a, hd, grid, st) != 0)
       return set_error(NSW_ERR_UNSUPPORTED, "%s: head_dim=%d unsupported (16, 32, 64, 128)", what, hd);
   } else {

@@ -196,9 +196,10 @@ def test_window_attention_kernels_agree(device, H, W, C, heads):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shift", [(0, 0), (4, 9)])
-def test_window_attention_windows_isolated(device, shift):
-    """bf16, head dim 64: a window's output depends on its own rows only.
+def test_window_attention_windows_isolated(device, shift, dtype):
+    """Head dim 64: a window's output depends on its own rows only.
     Every third window holds NaN; the others (including the last, whose
     padding rows lie past the end of qkv) must match the oracle.  512 windows
     x 2 heads, so that each CU runs several items and reuses its LDS after
@@ -208,14 +209,14 @@ def test_window_attention_windows_isolated(device, shift):
     L = ws[0] * ws[1]
     nW = (H // ws[0]) * (W // ws[1])
     g = torch.Generator().manual_seed(14)
-    qkv = torch.randn(nW, L, 3 * C, generator=g).to(torch.bfloat16)
+    qkv = torch.randn(nW, L, 3 * C, generator=g).to(dtype)
     bad = torch.arange(nW) % 3 == 1
     qkv[bad] = float("nan")
     scale = (C // heads) ** -0.5
     got = ops.window_attention(qkv.to(device), heads, scale, geometry=(H, W, ws, shift, 1)).cpu()
     want = attention_oracle(qkv, heads, scale, ref.make_attention_mask(H, W, ws, shift, 1))
     assert torch.isfinite(got[~bad]).all()
-    assert rel_l2(got[~bad], want[~bad]) < TOL[torch.bfloat16]
+    assert rel_l2(got[~bad], want[~bad]) < TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
