@@ -541,14 +541,24 @@ def model_sections(dev, steps, warmup, with_rollout=True):
         ev[0].record(stream)
         tok = model.prepare_tokens(x)
         ev[1].record(stream)
-        for blk in model.blocks:
-            tok = blk(tok)
+        tok = model.forward_blocks(tok)
         ev[2].record(stream)
         model._head_last(tok)
         ev[3].record(stream)
         torch.cuda.synchronize()
         if not torch.isfinite(yb.float()).all():
             raise RuntimeError("non-finite forecast")
+        # the same step with one fused call per block (no window-order chain)
+        model.chain_blocks = False
+        for _ in range(2):
+            model(x)
+        e0.record(stream)
+        for _ in range(steps):
+            model(x)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_per_block = e0.elapsed_time(e1) / steps
+        model.chain_blocks = True
     forecast = {
         "workload": "config 3: SwinTransformer fwd, [1,1,70,720,1440] -> [1,1,70,720,1440], p4 e1024 depth 16, "
                     "16 heads, window 9x18, alternating shift 0 / 4x9, coordinate pos-embed, bf16",
@@ -557,6 +567,7 @@ def model_sections(dev, steps, warmup, with_rollout=True):
         "tokens_per_s": round(tokens / (ms * 1e-3), 1),
         "embed_ms": round(ev[0].elapsed_time(ev[1]), 3), "blocks_ms": round(ev[1].elapsed_time(ev[2]), 3),
         "head_ms": round(ev[2].elapsed_time(ev[3]), 3),
+        "ms_per_step_block_calls": round(ms_per_block, 3),
     }
     del tok, yb
     if not with_rollout:

@@ -78,6 +78,16 @@ int nsw_window_reverse_roll(const void* windows, void* x, int64_t B, int64_t T, 
                             int64_t W, int64_t C, int64_t ws0, int64_t ws1, int64_t s0,
                             int64_t s1, int dtype, void* stream);
 
+/* nsw_roll_window_partition that also writes the partial sums of squares of
+ * every window-order row it stores: row_sumsq [B*T*H*W, nparts] fp32, part p
+ * = sum of the squares of the row's stored elements in bytes [512p, 512p+512)
+ * (nparts = ceil(C * dtype size / 512)).  The pre-pass of
+ * nsw_swin_blocks_forward: the tokens of models/swin.py:307-308's first
+ * block in its window order plus the norm1 statistics its QKV GEMM reads. */
+int nsw_window_partition_sumsq(const void* x, void* windows, float* row_sumsq, int64_t B, int64_t T,
+                               int64_t H, int64_t W, int64_t C, int64_t ws0, int64_t ws1, int64_t s0,
+                               int64_t s1, int dtype, void* stream);
+
 /* Block._make_attention_mask (models/swin_helpers.py:322-397), one GPU,
  * causal=False: writes the additive fp32 mask [nW, T*wa, T*wa], values
  * {0, -100}. */
@@ -204,6 +214,23 @@ size_t nsw_block_workspace_size(const nsw_block_shape* s);
 int nsw_swin_block_forward(const void* x, void* y, const nsw_block_params* p,
                            const nsw_block_shape* s, void* workspace, size_t workspace_bytes,
                            void* stream);
+
+/* Bytes of device workspace nsw_swin_blocks_forward needs for depth blocks of
+ * the shapes given (0 for a malformed shape). */
+size_t nsw_blocks_workspace_size(const nsw_block_shape* shapes, int64_t depth);
+
+/* The blocks loop of SwinTransformer.forward (models/swin.py:307-308,
+ * `for blk in self.blocks: x = blk(x)`): y = blocks[depth-1](...blocks[0](x)),
+ * x and y [B,T,H,W,C] in token order, must not alias.  The residual stream
+ * stays in window order between the blocks (each block's last GEMM stores its
+ * rows in the next block's window order together with their norm1
+ * statistics), so the result equals depth nsw_swin_block_forward calls up to
+ * the rounding of the folded norms.  Every block needs the norm-folded
+ * weights wqkv_n1 and w1_n2; all blocks share B,T,H,W,C, heads, window,
+ * hidden and dtype (shift and eps may differ).  1 + 5*depth launches. */
+int nsw_swin_blocks_forward(const void* x, void* y, const nsw_block_params* params,
+                            const nsw_block_shape* shapes, int64_t depth, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /* WeightedRMSE.forward (utils/losses.py:243-266) and the textbook weighted ACC.
  * pred/target fp32 [P, H, W] with P = B*T*Cch planes (channel = plane % Cch);

@@ -139,6 +139,16 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Sum over the 32 lanes [32h, 32h + 32) of a wavefront, valid on lanes 0 and
+// 32: each 16-lane row sum (row16_sum) plus that of the odd row next to it,
+// read with v_readlane (even row first).
+__device__ __forceinline__ float half32_sum_lead(float x, int lane) {
+  const float r = row16_sum(x);
+  const float o1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), 16));
+  const float o3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), 48));
+  return r + (lane & 32 ? o3 : o1);
+}
+
 __device__ __forceinline__ float rows4_max(float x) {
   float a = x, b = x;
   permlane16_swap(a, b);
@@ -273,7 +283,36 @@ struct WinGeom {
     return (int64_t)(((b * (uint32_t)T + t) * (uint32_t)H + (uint32_t)h) * (uint32_t)W + (uint32_t)w);
   }
 
-  __device__ __forceinline__ int64_t row_of_token(int64_t tok) const {
+  __device__ __forceinline__ int64_t row_of_token(int64_t tok) const { return row_of_token_shift(tok, s0, s1); }
+
+  // Window-ordered row m of this geometry -> the row of the same token in
+  // the window order of the image rolled by (sa, sb) instead of (s0, s1),
+  // with dh = (s0 - sa) mod H, dw = (s1 - sb) mod W: the token's rolled
+  // position moves by (dh, dw), so row_of_token_shift(token_of_row(m), sa,
+  // sb) without forming the token (7 divisions by constants instead of 10).
+  __device__ __forceinline__ int64_t row_of_row_shift(int64_t m, int dh, int dw) const {
+    const uint32_t mu = (uint32_t)m;
+    const uint32_t win = dL.div(mu);
+    const uint32_t p = mu - win * (uint32_t)L;
+    const uint32_t t = dwa.div(p);
+    const uint32_t rr = p - t * (uint32_t)wa;
+    const uint32_t r = dws1.div(rr);
+    const uint32_t c = rr - r * (uint32_t)ws1;
+    const uint32_t b = dnW.div(win);
+    const uint32_t wi = win - b * (uint32_t)nW;
+    const uint32_t i = dnwb.div(wi);
+    const uint32_t j = wi - i * (uint32_t)nwb;
+    int h = (int)(i * ws0 + r) + dh; if (h >= H) h -= H;
+    int w = (int)(j * ws1 + c) + dw; if (w >= W) w -= W;
+    const uint32_t i2 = dws0.div((uint32_t)h), r2 = (uint32_t)h - i2 * (uint32_t)ws0;
+    const uint32_t j2 = dws1.div((uint32_t)w), c2 = (uint32_t)w - j2 * (uint32_t)ws1;
+    const uint32_t win2 = b * (uint32_t)nW + i2 * (uint32_t)nwb + j2;
+    return (int64_t)((win2 * (uint32_t)T + t) * (uint32_t)wa + r2 * (uint32_t)ws1 + c2);
+  }
+
+  // row_of_token of the same geometry rolled by (sa, sb) in [0, H) x [0, W)
+  // instead of (s0, s1): the window order of another block of the image.
+  __device__ __forceinline__ int64_t row_of_token_shift(int64_t tok, int sa, int sb) const {
     const uint32_t tu = (uint32_t)tok;
     const uint32_t bt = dHW.div(tu);
     const uint32_t hw = tu - bt * (uint32_t)H * (uint32_t)W;
@@ -281,8 +320,8 @@ struct WinGeom {
     const uint32_t w = hw - h * (uint32_t)W;
     const uint32_t b = dT.div(bt);
     const uint32_t t = bt - b * (uint32_t)T;
-    int hs = (int)h - s0; if (hs < 0) hs += H;
-    int wsft = (int)w - s1; if (wsft < 0) wsft += W;
+    int hs = (int)h - sa; if (hs < 0) hs += H;
+    int wsft = (int)w - sb; if (wsft < 0) wsft += W;
     const uint32_t i = dws0.div((uint32_t)hs), r = (uint32_t)hs - i * (uint32_t)ws0;
     const uint32_t j = dws1.div((uint32_t)wsft), c = (uint32_t)wsft - j * (uint32_t)ws1;
     const uint32_t win = b * (uint32_t)nW + i * (uint32_t)nwb + j;

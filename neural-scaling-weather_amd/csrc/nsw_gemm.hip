@@ -417,8 +417,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
   constexpr int BATCH = ITER < 8 ? ITER : 8;
   constexpr int NBAT = ITER / BATCH;
   static_assert(ITER % BATCH == 0, "batch");
-  constexpr bool RES = EPI == EPI_BIAS_RESIDUAL || EPI == EPI_SCATTER_RESIDUAL;
   constexpr bool SCAT = EPI == EPI_SCATTER_RESIDUAL;
+  constexpr bool REMAP = EPI == EPI_REMAP_RESIDUAL;
+  constexpr bool TOK = EPI == EPI_TOKEN_RESIDUAL;
+  constexpr bool RES = EPI == EPI_BIAS_RESIDUAL || SCAT || REMAP || TOK || EPI == EPI_RES_SUMSQ;
+  // row sums of squares of the stored rows (optional for the scatter)
+  constexpr bool SUMSQ = SCAT || REMAP || EPI == EPI_RES_SUMSQ;
   NSW_WAIT_VMCNT(0);                                  // the copies past the last stage
   NSW_WAIT_LGKMCNT0();
   wg_barrier();                                       // the operand ring is no longer read
@@ -465,16 +469,42 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
     const int prow0 = pass * S::ROWS;                 // first tile row of this pass
     int orow[2][BATCH];                               // output row (token for the scatter) per batch row
     u32x4 rres[2][RES ? BATCH : 1];
+    // Row maps: the wave copies ITER * RPI (<= 64) consecutive rows per pass,
+    // so lane l maps the wave's row l once and every copy instruction takes
+    // its rows' targets from those lanes (v_readlane) instead of all 32 or
+    // 64 lanes of a row evaluating the same map.
+    constexpr bool MAPPED = SCAT || TOK || REMAP;
+    constexpr int WROWS = ITER * RPI;                 // rows per wave per pass
+    static_assert(WROWS <= 64, "one row per lane");
+    int lmap = 0;
+    if constexpr (MAPPED) {
+      int mm = m0 + prow0 + wave * WROWS + (lane % WROWS);
+      mm = mm < M ? mm : M - 1;
+      if constexpr (REMAP) lmap = (int)ea.geom.row_of_row_shift(mm, ea.dh, ea.dw);
+      else lmap = (int)ea.geom.token_of_row(mm);
+    }
     auto prefetch = [&](int ib, int slot) {
 #pragma unroll
       for (int b = 0; b < BATCH; ++b) {
-        const int rl = (wave * ITER + ib * BATCH + b) * RPI + lrow;
+        const int q = ib * BATCH + b;                 // copy instruction of the pass (unrolled: constant)
+        const int rl = (wave * ITER + q) * RPI + lrow;
         int m = m0 + prow0 + rl;
         m = m < M ? m : M - 1;
-        if constexpr (SCAT) orow[slot][b] = (int)ea.geom.token_of_row(m);
-        else orow[slot][b] = m;
+        if constexpr (MAPPED) {
+          const int a0 = __builtin_amdgcn_readlane(lmap, q * RPI);
+          if constexpr (RPI == 2) {
+            const int a1 = __builtin_amdgcn_readlane(lmap, q * RPI + 1);
+            orow[slot][b] = lrow ? a1 : a0;
+          } else {
+            orow[slot][b] = a0;
+          }
+        } else {
+          orow[slot][b] = m;
+        }
+        // the residual row: the output row for the scatter, row m otherwise
+        const int rrow = SCAT ? orow[slot][b] : m;
         if constexpr (RES)
-          rres[slot][b] = *reinterpret_cast<const u32x4*>((const T*)ea.residual + (int64_t)orow[slot][b] * N + nc);
+          rres[slot][b] = *reinterpret_cast<const u32x4*>((const T*)ea.residual + (int64_t)rrow * N + nc);
       }
     };
     prefetch(0, 0);
@@ -521,7 +551,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
 #pragma unroll
           for (int e = 0; e < VEC; ++e) o[e] += rv[e];
           if (ok) store16<T>(Y + (int64_t)orow[cur][b] * N + n, o);
-          if constexpr (SCAT) {
+          if constexpr (SUMSQ) {
             // only stored elements count (lanes past N or rows past M add 0)
 #pragma unroll
             for (int e = 0; e < VEC; ++e) {
@@ -533,13 +563,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
         } else {
           if (ok) *reinterpret_cast<u32x4*>(Y + (int64_t)orow[cur][b] * N + n) = ov[b];
         }
-        if constexpr (SCAT) {
+        if constexpr (SUMSQ) {
           // partial sum of squares over 32 lanes (32 * VEC columns: two DPP
           // rows, even row first), one float per 512 bytes of output row
-          if (ea.row_sumsq != nullptr) {
-            float lo16 = row16_sum(ssq), hi16 = lo16;
-            permlane16_swap(lo16, hi16);
-            ssq = lo16 + hi16;
+          if (!SCAT || ea.row_sumsq != nullptr) {
+            ssq = half32_sum_lead(ssq, lane);
             if ((lane & 31) == 0 && ok)
               ea.row_sumsq[(int64_t)orow[cur][b] * ea.nparts + n / (32 * VEC)] = ssq;
           }
@@ -676,6 +704,67 @@ int gemm_qkv_norm_gather(const void* x, const void* wqkv_n, const void* bqkv, co
   if (hd == 32)
     return dispatch_gemm<EPI_QKV_HN32, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
   return dispatch_gemm<EPI_QKV_HN16, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+}
+
+// QKV projection of rows whose RMSNorm (norm1) comes as a row scale from the
+// producer's partial sums of squares: qkv[m] = headnorm(rs1[m] * (x[m] .
+// wqkv_n^T) + b), wqkv_n = wqkv * norm1_w per input column, rs1 =
+// 1/sqrt(sum_p row_sumsq[m, p] / C + eps).  Rows in any order.
+int gemm_qkv_rowscale(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w, const void* kn_w,
+                      float eps, void* qkv, const float* row_sumsq, int64_t nparts, int64_t M, int64_t C,
+                      int64_t num_heads, int dtype, void* stream) {
+  const char* what = "nsw_qkv_projection_rowscale";
+  NSW_CHECK_ARG(num_heads > 0 && C % num_heads == 0, "%s: C=%lld not divisible by num_heads=%lld", what,
+                (long long)C, (long long)num_heads);
+  const int64_t hd = C / num_heads;
+  NSW_CHECK_ARG(C % 64 == 0, "%s: C=%lld must be a multiple of 64", what, (long long)C);
+  NSW_CHECK_ARG(hd == 16 || hd == 32 || hd == 64, "%s: head_dim=%lld unsupported (16, 32, 64)", what,
+                (long long)hd);
+  NSW_CHECK_ARG(bqkv && qn_w && kn_w, "%s: bias and norm weights are required", what);
+  NSW_CHECK_ARG(row_sumsq != nullptr && nparts > 0 && nparts <= 4096 && ((uintptr_t)row_sumsq % 16) == 0,
+                "%s: row_sumsq [M, nparts] (16-byte aligned) is required", what);
+  EpiArgs ea{};
+  ea.bias = bqkv; ea.qn_w = qn_w; ea.kn_w = kn_w; ea.eps = eps; ea.C = (int)C;
+  ea.row_sumsq = const_cast<float*>(row_sumsq);
+  ea.nparts = (int)nparts;
+  if (hd == 64) return dispatch_gemm<EPI_QKV_HN64, PRE_ROWSCALE>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+  if (hd == 32) return dispatch_gemm<EPI_QKV_HN32, PRE_ROWSCALE>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+  return dispatch_gemm<EPI_QKV_HN16, PRE_ROWSCALE>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+}
+
+// y[remap(m)] = x[m] . w^T + bias + residual[m], the stored rows' partial
+// sums of squares (one float per 512 bytes of row) into row_sumsq at the
+// same rows where asked.  map_mode 0: remap(m) = m (row_sumsq required); 1:
+// the token of window-order row m of the image geometry (B, T, H, W, ws,
+// shift s) (no row sums); 2: that token's row in the window order of the
+// same image rolled by (sa, sb), the next block's (row_sumsq required).
+int gemm_linear_remap(const void* x, const void* w, const void* bias, const void* residual, void* y,
+                      float* row_sumsq, int64_t M, int64_t N, int64_t K, int map_mode, int64_t B, int64_t T,
+                      int64_t H, int64_t W, int64_t ws0, int64_t ws1, int64_t s0, int64_t s1, int64_t sa,
+                      int64_t sb, int dtype, void* stream) {
+  const char* what = "nsw_linear_remap_residual";
+  NSW_CHECK_ARG(bias && residual, "%s: bias and residual are required", what);
+  NSW_CHECK_ARG(residual != (const void*)y, "%s: residual and y must not alias", what);
+  NSW_CHECK_ARG(map_mode >= 0 && map_mode <= 2, "%s: map_mode must be 0, 1 or 2", what);
+  NSW_CHECK_ARG((row_sumsq != nullptr) == (map_mode != 1),
+                "%s: row sums of squares are written for map modes 0 and 2 only, and required there", what);
+  EpiArgs ea{};
+  ea.bias = bias; ea.residual = residual;
+  if (map_mode != 0) {
+    int rc = check_geom(B, T, H, W, ws0, ws1, what);
+    if (rc) return rc;
+    NSW_CHECK_ARG(M == B * T * H * W, "%s: M must be B*T*H*W for a row map", what);
+    ea.geom = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
+    const int64_t a = ((sa % H) + H) % H, b = ((sb % W) + W) % W;
+    ea.dh = (int)(((ea.geom.s0 - a) % H + H) % H);
+    ea.dw = (int)(((ea.geom.s1 - b) % W + W) % W);
+  }
+  ea.row_sumsq = row_sumsq;
+  ea.nparts = (int)sumsq_parts(N, dtype);
+  if (row_sumsq) NSW_CHECK_ARG(((uintptr_t)row_sumsq % 4) == 0, "%s: row_sumsq must be 4-byte aligned", what);
+  if (map_mode == 0) return dispatch_gemm<EPI_RES_SUMSQ>(dtype, x, w, y, M, N, K, ea, stream, what);
+  if (map_mode == 1) return dispatch_gemm<EPI_TOKEN_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);
+  return dispatch_gemm<EPI_REMAP_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);
 }
 
 // y = epi(RMSNorm(x) . W^T) with w_n = W * norm_w: the row norm of x fused.

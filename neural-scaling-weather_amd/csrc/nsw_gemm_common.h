@@ -14,6 +14,9 @@ enum Epi {
   EPI_BIAS_RESIDUAL = NSW_EPI_BIAS_RESIDUAL,
   EPI_BIAS_GELU_TANH = NSW_EPI_BIAS_GELU_TANH,
   EPI_SCATTER_RESIDUAL = 11, // bias, row m -> token_of_row(m), + skip[token]
+  EPI_REMAP_RESIDUAL = 12,   // bias, + residual[m], stored at row_of_row_shift(m), + row sums of squares
+  EPI_RES_SUMSQ = 13,        // bias, + residual[m], stored at row m, + row sums of squares
+  EPI_TOKEN_RESIDUAL = 14,   // bias, + residual[m], stored at token_of_row(m)
   EPI_QKV_HN16 = 16,         // bias, then per-head RMSNorm of the q and k
   EPI_QKV_HN32 = 32,         // columns, for head dims 16 / 32 / 64
   EPI_QKV_HN64 = 64
@@ -49,8 +52,11 @@ struct EpiArgs {
   float eps;
   int C;       // q/k/v width for the QKV epilogues
   WinGeom geom;  // EPI_SCATTER_RESIDUAL
-  float* row_sumsq;   // scatter epilogue: optional [tokens, nparts] output; PRE_ROWSCALE: input
+  // [rows, nparts] row sums of squares: output of EPI_SCATTER_RESIDUAL
+  // (optional), EPI_REMAP_RESIDUAL and EPI_RES_SUMSQ; input of PRE_ROWSCALE
+  float* row_sumsq;
   int nparts;
+  int dh, dw;   // EPI_REMAP_RESIDUAL: shift differences of geom.row_of_row_shift
 };
 
 // GELU with the exact-erf form of nn.GELU(): 0.5 v (1 + erf(v / sqrt 2)).

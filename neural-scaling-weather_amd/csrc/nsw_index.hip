@@ -78,6 +78,39 @@ __global__ __launch_bounds__(256) void row_map_kernel(const T* __restrict__ x,
   }
 }
 
+// Window partition (the roll by -shift folded in) that also writes the
+// rows' partial sums of squares, one float per 512 bytes of row (the layout
+// the row-scaled GEMMs read): in chunk iteration k, lanes 0-31 and 32-63
+// cover parts 2k and 2k+1 (32 lanes x 16 B), summed as the GEMM epilogues
+// sum theirs (FMA chain per lane, DPP row sums, even row first).
+template <typename T, int CH>
+__global__ __launch_bounds__(256) void partition_sumsq_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                              float* __restrict__ ss, int nparts, int64_t rows,
+                                                              int C, WinGeom g) {
+  constexpr int VEC = Vec16<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= rows) return;   // whole waves: the DPP sums below see every lane
+  const T* xr = x + g.token_of_row(m) * C;
+  T* yr = y + m * C;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int c0 = (lane + 64 * k) * VEC;
+    float part = 0.f;
+    if (c0 < C) {
+      float v[VEC];
+      load16<T>(xr + c0, v);
+      store16<T>(yr + c0, v);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) part = fmaf(v[e], v[e], part);
+    }
+    float lo = row16_sum(part), hi = lo;
+    permlane16_swap(lo, hi);
+    const int p = 2 * k + (lane >> 5);
+    if ((lane & 31) == 0 && p < nparts) ss[m * nparts + p] = lo + hi;
+  }
+}
+
 template <typename T, int MAP, bool NORM>
 static int launch_row_map(const void* x, const void* w, float eps, void* y, int64_t rows,
                           int64_t C, const WinGeom& g, hipStream_t st, const char* what) {
@@ -252,6 +285,52 @@ extern "C" int nsw_rmsnorm_roll_partition(const void* x, const void* w, float ep
   WinGeom g = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
   return dispatch_row_map<MAP_PARTITION, true>(dtype, x, w, eps, xw, B * T * H * W, C, g, stream,
                                                "nsw_rmsnorm_roll_partition");
+}
+
+namespace nsw {
+int64_t sumsq_parts(int64_t C, int dtype);
+
+template <typename T>
+static int launch_partition_sumsq(const void* x, void* xw, float* ss, int64_t rows, int64_t C, int nparts,
+                                  const WinGeom& g, hipStream_t st, const char* what) {
+  constexpr int VEC = Vec16<T>::N;
+  NSW_CHECK_ARG(C > 0 && C % VEC == 0, "%s: C=%lld must be a positive multiple of %d", what, (long long)C, VEC);
+  NSW_CHECK_ARG(((uintptr_t)x % 16) == 0 && ((uintptr_t)xw % 16) == 0 && ((uintptr_t)ss % 4) == 0,
+                "%s: pointers must be 16-byte (row_sumsq 4-byte) aligned", what);
+  if (rows == 0) return NSW_OK;
+  const int64_t per_lane = (C / VEC + 63) / 64;
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  const T* xp = (const T*)x;
+  T* yp = (T*)xw;
+  if (per_lane <= 1)
+    hipLaunchKernelGGL((partition_sumsq_kernel<T, 1>), grid, block, 0, st, xp, yp, ss, nparts, rows, (int)C, g);
+  else if (per_lane <= 2)
+    hipLaunchKernelGGL((partition_sumsq_kernel<T, 2>), grid, block, 0, st, xp, yp, ss, nparts, rows, (int)C, g);
+  else if (per_lane <= 4)
+    hipLaunchKernelGGL((partition_sumsq_kernel<T, 4>), grid, block, 0, st, xp, yp, ss, nparts, rows, (int)C, g);
+  else if (per_lane <= 8)
+    hipLaunchKernelGGL((partition_sumsq_kernel<T, 8>), grid, block, 0, st, xp, yp, ss, nparts, rows, (int)C, g);
+  else
+    return set_error(NSW_ERR_UNSUPPORTED, "%s: C=%lld too large", what, (long long)C);
+  return check_launch(what);
+}
+
+}  // namespace nsw
+
+extern "C" int nsw_window_partition_sumsq(const void* x, void* xw, float* row_sumsq, int64_t B, int64_t T,
+                                          int64_t H, int64_t W, int64_t C, int64_t ws0, int64_t ws1, int64_t s0,
+                                          int64_t s1, int dtype, void* stream) {
+  const char* what = "nsw_window_partition_sumsq";
+  int rc = check_geom(B, T, H, W, ws0, ws1, what);
+  if (rc) return rc;
+  NSW_CHECK_ARG(x && xw && row_sumsq && x != (const void*)xw, "%s: x, xw, row_sumsq required, x != xw", what);
+  const WinGeom g = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
+  const int64_t rows = B * T * H * W;
+  const int nparts = (int)sumsq_parts(C, dtype);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == NSW_DTYPE_BF16) return launch_partition_sumsq<bf16>(x, xw, row_sumsq, rows, C, nparts, g, st, what);
+  if (dtype == NSW_DTYPE_F32) return launch_partition_sumsq<float>(x, xw, row_sumsq, rows, C, nparts, g, st, what);
+  return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, dtype);
 }
 
 extern "C" int nsw_make_attention_mask(float* mask, int64_t H, int64_t W, int64_t ws0, int64_t ws1,

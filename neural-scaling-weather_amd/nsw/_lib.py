@@ -70,6 +70,11 @@ SIGNATURES = {
     "nsw_block_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(BlockShape)]),
     "nsw_swin_block_forward": (_int, [_vp, _vp, ctypes.POINTER(BlockParams), ctypes.POINTER(BlockShape),
                                       _vp, ctypes.c_size_t, _vp]),
+    "nsw_blocks_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(BlockShape), _i64]),
+    "nsw_swin_blocks_forward": (_int, [_vp, _vp, ctypes.POINTER(BlockParams), ctypes.POINTER(BlockShape), _i64,
+                                       _vp, ctypes.c_size_t, _vp]),
+    "nsw_window_partition_sumsq": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                          _int, _vp]),
     "nsw_weighted_metrics_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "nsw_weighted_metrics": (_int, [_vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp,
                                     ctypes.c_size_t, _vp]),

@@ -411,6 +411,55 @@ def swin_block_forward(x: torch.Tensor, packed: dict, num_heads: int, window_siz
     return y
 
 
+def swin_blocks_forward(x: torch.Tensor, packs, num_heads: int, window_size, shifts, eps: Optional[float] = None,
+                        out: Optional[torch.Tensor] = None, gelu_tanh: bool = False) -> torch.Tensor:
+    """The blocks loop ``for blk in blocks: x = blk(x)`` through one C-ABI
+    call that keeps the residual stream in window order between blocks.
+    ``packs[i]`` is block i's dict of nsw_block_params tensors and must hold
+    the norm-folded ``wqkv_n1`` and ``w1_n2``; ``shifts[i]`` its shift."""
+    packs = list(packs)
+    if not packs or len(packs) != len(shifts):
+        raise ValueError("swin_blocks_forward: one pack and one shift per block")
+    tensors = [t for pk in packs for t in pk.values()]
+    dev = _dev(x, *tensors)
+    _same_dtype(x, *tensors)
+    if x.dim() != 5 or not x.is_contiguous():
+        raise ValueError("swin_blocks_forward: x must be a contiguous [B, T, H, W, C] tensor")
+    depth = len(packs)
+    hidden = packs[0]["w1"].shape[0]
+    shapes = (_lib.BlockShape * depth)(*[block_shape(x, num_heads, window_size, shifts[i], hidden, eps, gelu_tanh)
+                                         for i in range(depth)])
+    params = (_lib.BlockParams * depth)(*[_lib.BlockParams(*[_p(pk.get(n)) for n, _ in _lib.BlockParams._fields_])
+                                          for pk in packs])
+    nbytes = lib().nsw_blocks_workspace_size(shapes, depth)
+    if nbytes == 0:
+        raise ValueError("swin_blocks_forward: malformed block shape")
+    ws = workspace(nbytes, dev)
+    y = torch.empty_like(x) if out is None else out
+    check(lib().nsw_swin_blocks_forward(x.data_ptr(), y.data_ptr(), params, shapes, depth, ws.data_ptr(),
+                                        ws.numel(), _stream(dev)), "swin_blocks_forward")
+    return y
+
+
+def window_partition_sumsq(x: torch.Tensor, window_size, shift_size):
+    """(windows, row_sumsq): x [B,T,H,W,C] rolled by -shift and split into
+    windows [B*nW, T, ws0, ws1, C], and fp32 [rows, nparts] partial sums of
+    squares of each stored row (512-byte parts)."""
+    dev = _dev(x)
+    if x.dim() != 5 or not x.is_contiguous():
+        raise ValueError("window_partition_sumsq: x must be a contiguous [B, T, H, W, C] tensor")
+    B, T, H, W, C = x.shape
+    ws0, ws1 = window_size
+    nW = (H // ws0) * (W // ws1)
+    xw = torch.empty((B * nW, T, ws0, ws1, C), dtype=x.dtype, device=dev)
+    nparts = lib().nsw_row_sumsq_parts(C, dtype_code(x))
+    ss = torch.empty((x.numel() // C, nparts), dtype=torch.float32, device=dev)
+    check(lib().nsw_window_partition_sumsq(x.data_ptr(), xw.data_ptr(), ss.data_ptr(), B, T, H, W, C, ws0, ws1,
+                                           int(shift_size[0]), int(shift_size[1]), dtype_code(x), _stream(dev)),
+          "window_partition_sumsq")
+    return xw, ss
+
+
 # ----------------------------------------------------------------- metrics ---
 
 def weighted_metrics(pred: torch.Tensor, target: torch.Tensor, weights: torch.Tensor,

@@ -220,6 +220,12 @@ class SwinTransformer(nn.Module):
         self.out_size = out_chans * patch_size * patch_size
         self.head = LinearLayer(embed_dim, self.out_size, comm_metadata=dict(_EMBED_META))
         self.apply(self._init_weights)
+        # chain_blocks: run the blocks loop as one C-ABI call that keeps the
+        # residual stream in window order between blocks (each block's fc2
+        # stores its rows in the next block's window order with their norm1
+        # statistics: no per-block gather / scatter / norm passes, 1 + 5 *
+        # depth launches).  False: one fused call per block.
+        self.chain_blocks = True
         self._pos_key = None
         self._pos = None
 
@@ -305,9 +311,27 @@ class SwinTransformer(nn.Module):
         frame t is read from slot (t + frame0) mod T of x, and ``out`` receives
         the prediction (any float dtype; e.g. a slot of the input ring)."""
         y = self.prepare_tokens(x, invariants=invariants, frame0=frame0)
-        for blk in self.blocks:
-            y = blk(y)
+        y = self.forward_blocks(y)
         return self._head_last(y, out=out)
+
+    def forward_blocks(self, y: torch.Tensor) -> torch.Tensor:
+        """``for blk in self.blocks: y = blk(y)`` (models/swin.py:307-308),
+        through the window-order chain when ``chain_blocks`` is set."""
+        if not self.chain_blocks or len(self.blocks) == 0:
+            for blk in self.blocks:
+                y = blk(y)
+            return y
+        b0 = self.blocks[0]
+        for blk in self.blocks:
+            blk.check_input(y)
+        eps = {blk._eps(y.dtype) for blk in self.blocks}
+        tanh = {blk.mlp.gelu_tanh for blk in self.blocks}
+        if len(eps) != 1 or len(tanh) != 1:
+            raise NotImplementedError("the block chain needs one eps and one GELU form for all blocks")
+        packs = [blk.packed(fold_all=True) for blk in self.blocks]
+        shifts = [blk.shift_size for blk in self.blocks]
+        return ops.swin_blocks_forward(y.contiguous(), packs, b0.num_heads, b0.window_size, shifts,
+                                       eps=eps.pop(), gelu_tanh=tanh.pop())
 
 
 class TimeStepper(nn.Module):

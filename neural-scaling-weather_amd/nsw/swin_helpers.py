@@ -197,7 +197,10 @@ class Block(nn.Module):
             raise NotImplementedError("the fused block needs one eps for all four RMSNorms")
         return es.pop()
 
-    def packed(self):
+    def packed(self, fold_all: bool = False):
+        """Tensors named like the fields of nsw_block_params.  The norm-folded
+        weights are included as fold_norm1 / fold_norm2 ask, or both when
+        ``fold_all`` (the window-order chain of SwinTransformer.forward)."""
         a = self.attn
         ps = [self.norm1.norm.weight, a.q.weight, a.k.weight, a.v.weight, a.biasq.bias, a.biask.bias,
               a.biasv.bias, a.q_norm.norm.weight, a.k_norm.norm.weight, a.proj.weight, a.biasproj.bias,
@@ -219,13 +222,20 @@ class Block(nn.Module):
         with torch.no_grad():
             # norm weights folded into the GEMM weights that consume the
             # normalised rows: RMSNorm(x) . W^T = rs(x) * (x . (W * norm_w)^T)
-            if self.fold_norm1 and "wqkv_n1" not in pk:
+            if (self.fold_norm1 or fold_all) and "wqkv_n1" not in pk:
                 n1 = pk["norm1_w"].float()
                 pk["wqkv_n1"] = (pk["wqkv"].float() * n1[None, :]).to(pk["wqkv"].dtype).contiguous()
-            if self.fold_norm2 and "w1_n2" not in pk:
+            if (self.fold_norm2 or fold_all) and "w1_n2" not in pk:
                 n2 = pk["norm2_w"].float()
                 pk["w1_n2"] = (pk["w1"].float() * n2[None, :]).to(pk["w1"].dtype).contiguous()
         return self._pack
+
+    def check_input(self, x: torch.Tensor) -> None:
+        if x.dim() != 5 or tuple(x.shape[2:4]) != self.feat_size:
+            raise ValueError(f"expected [B, T, {self.feat_size[0]}, {self.feat_size[1]}, C], got {tuple(x.shape)}")
+        if x.shape[1] != self.temporal_context_window_size:
+            raise ValueError("temporal dim does not match temporal_context_window_size")
+        self.mlp._check_fusable()
 
     def _shifted_window_attn(self, x: torch.Tensor) -> torch.Tensor:
         """models/swin_helpers.py:399-433 on an already-normalised x."""
@@ -238,11 +248,7 @@ class Block(nn.Module):
 
     def forward(self, x: torch.Tensor, condition: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x [B, T, H, W, C] -> [B, T, H, W, C] (models/swin_helpers.py:435-459)."""
-        if x.dim() != 5 or tuple(x.shape[2:4]) != self.feat_size:
-            raise ValueError(f"expected [B, T, {self.feat_size[0]}, {self.feat_size[1]}, C], got {tuple(x.shape)}")
-        if x.shape[1] != self.temporal_context_window_size:
-            raise ValueError("temporal dim does not match temporal_context_window_size")
-        self.mlp._check_fusable()
+        self.check_input(x)
         pk = self.packed()
         drop = ([] if self.fold_norm1 else ["wqkv_n1"]) + ([] if self.fold_norm2 else ["w1_n2"])
         if drop:

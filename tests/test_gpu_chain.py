@@ -1,0 +1,173 @@
+"""GPU parity of the blocks loop of SwinTransformer.forward (models/swin.py:
+307-308, ``for blk in self.blocks: x = blk(x)``) run as one window-order
+chain (nsw_swin_blocks_forward): the fp32 CPU oracle applies the reference
+block (models/swin_helpers.py:435-459) depth times in token order.
+
+Tolerances: fp32 relative L2 <= 1e-5 per block of depth (the block's bar,
+north_star's fp32 parity mode); bf16 relative L2 <= 1e-2 of the output
+(north_star's bf16 bar, the same as one block) and the chain's error no
+more than 1.25x that of depth separate fused block calls on the same
+inputs.  The chain equals the separate calls up to rounding (same
+arithmetic, norms applied as row scales), checked in fp32 at 2e-6."""
+import pytest
+import torch
+
+from oracle import swin_ref as ref
+from oracle import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_l2(a, b):
+    a = a.double().cpu()
+    b = b.double().cpu()
+    return (torch.linalg.vector_norm(a - b) / torch.linalg.vector_norm(b)).item()
+
+
+def make_stack(device, dtype, T, H, W, C, heads, ws, shifts, seed):
+    import nsw
+    blocks, params = [], []
+    for i, sh in enumerate(shifts):
+        p = synth.block_params(C, heads, seed=100 * seed + i, random_bias=True, random_norm=True)
+        p = {k: v.to(dtype).float() for k, v in p.items()}
+        blk = nsw.Block(C, heads, (H, W), ws, T, shift_size=sh)
+        blk.load_state_dict(p)
+        blocks.append(blk.to(device=device, dtype=dtype))
+        params.append(p)
+    return blocks, params
+
+
+def run_chain(blocks, x):
+    from nsw import ops
+    b0 = blocks[0]
+    packs = [b.packed(fold_all=True) for b in blocks]
+    return ops.swin_blocks_forward(x, packs, b0.num_heads, b0.window_size, [b.shift_size for b in blocks],
+                                   eps=b0._eps(x.dtype), gelu_tanh=b0.mlp.gelu_tanh)
+
+
+def oracle_stack(x, params, heads, ws, shifts, eps, device=None):
+    y = x
+    for p, sh in zip(params, shifts):
+        if device is not None:
+            p = {k: v.to(device) for k, v in p.items()}
+        y = ref.block_forward(y, p, heads, ws, sh, eps=eps)
+    return y
+
+
+ALT = [(0, 0), (4, 9)]
+
+FP32_CASES = [
+    # B, T, H, W, C, heads, ws, shifts
+    (1, 1, 90, 180, 192, 6, (9, 18), ALT * 2),
+    (2, 1, 18, 36, 128, 2, (9, 18), ALT * 2 + [(0, 0)]),
+    (1, 2, 18, 36, 128, 4, (9, 18), [(4, 9), (4, 9), (2, 5), (0, 0)]),   # equal and arbitrary shifts
+    (1, 1, 16, 32, 64, 4, (4, 8), [(2, 4)]),                             # depth 1
+]
+
+
+@pytest.mark.parametrize("B,T,H,W,C,heads,ws,shifts", FP32_CASES)
+def test_chain_fp32(device, B, T, H, W, C, heads, ws, shifts):
+    blocks, params = make_stack(device, torch.float32, T, H, W, C, heads, ws, shifts, seed=B * 7 + T)
+    x = synth.activations((B, T, H, W, C), seed=11 * B + T)
+    with torch.inference_mode():
+        xd = x.to(device)
+        y = run_chain(blocks, xd)
+        y_sep = xd
+        for blk in blocks:
+            y_sep = blk(y_sep)
+    torch.cuda.synchronize()
+    want = oracle_stack(x, params, heads, ws, shifts, torch.finfo(torch.float32).eps)
+    assert rel_l2(y, want) < 1e-5 * len(shifts)
+    assert rel_l2(y - x.to(device), want - x) < 1e-4 * len(shifts)
+    assert rel_l2(y, y_sep) < 2e-6
+
+
+def test_chain_bf16_config2(device):
+    """Four blocks at config 2's geometry (180x360, C=1024, 16 heads, window
+    9x18, alternating shift), bf16; oracle in fp32 on the device."""
+    T, H, W, C, heads, ws = 1, 180, 360, 1024, 16, (9, 18)
+    shifts = ALT * 2
+    blocks, params = make_stack(device, torch.bfloat16, T, H, W, C, heads, ws, shifts, seed=5)
+    x = synth.activations((1, T, H, W, C), seed=55).to(torch.bfloat16).float()
+    with torch.inference_mode():
+        xd = x.to(device, torch.bfloat16)
+        y = run_chain(blocks, xd).float()
+        y_sep = xd
+        for blk in blocks:
+            y_sep = blk(y_sep)
+        y_sep = y_sep.float()
+        want = oracle_stack(x.to(device), params, heads, ws, shifts, torch.finfo(torch.bfloat16).eps,
+                            device=device)
+    torch.cuda.synchronize()
+    e_chain, e_sep = rel_l2(y, want), rel_l2(y_sep, want)
+    assert e_chain < 1e-2
+    assert e_chain < 1.25 * e_sep
+
+
+def test_chain_input_untouched_and_repeatable(device):
+    """x is read only; two calls give identical results (no state kept in
+    the shared workspace between calls)."""
+    shifts = ALT * 2
+    blocks, _ = make_stack(device, torch.bfloat16, 1, 18, 36, 128, 2, (9, 18), shifts, seed=9)
+    x = synth.activations((1, 1, 18, 36, 128), seed=99).to(device, torch.bfloat16)
+    x0 = x.clone()
+    with torch.inference_mode():
+        y1 = run_chain(blocks, x)
+        y2 = run_chain(blocks, x)
+    torch.cuda.synchronize()
+    assert torch.equal(x, x0)
+    assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shift", [(0, 0), (4, 9)])
+def test_window_partition_sumsq(device, dtype, shift):
+    """Rows equal the fused roll + partition bit for bit; each 512-byte part's
+    sum of squares equals the float64 sum of the stored values' squares."""
+    from nsw import ops
+    B, T, H, W, C, ws = 2, 1, 18, 36, 320, (9, 18)
+    x = synth.activations((B, T, H, W, C), seed=3).to(device, dtype)
+    with torch.inference_mode():
+        xw, ss = ops.window_partition_sumsq(x, ws, shift)
+        want_w = ops.roll_window_partition(x, ws, shift)
+    torch.cuda.synchronize()
+    assert torch.equal(xw, want_w)
+    per = 512 // x.element_size()
+    rows = xw.reshape(-1, C).double().cpu()
+    nparts = -(-C // per)
+    assert ss.shape == (rows.shape[0], nparts)
+    want = torch.stack([(rows[:, p * per:(p + 1) * per] ** 2).sum(1) for p in range(nparts)], 1)
+    torch.testing.assert_close(ss.double().cpu(), want, rtol=2e-6, atol=1e-6)
+
+
+def test_model_chain_matches_block_calls(device):
+    """SwinTransformer.forward with chain_blocks on and off (small model,
+    fp32): the same prediction up to rounding."""
+    import nsw
+    H, W, p, C = 72, 144, 4, 5
+    meta = {"coords": torch.randn(H, W, 3), "sp_shapes": [[H], [W]], "n_channels": C}
+    torch.manual_seed(4)
+    model = nsw.SwinTransformer(window_size=(9, 18), patch_size=p, in_chans=C, out_chans=C, embed_dim=128,
+                                depth=4, num_heads=2, domain_metadata=meta).to(device).eval()
+    x = torch.randn(1, 1, C, H, W, device=device)
+    with torch.inference_mode():
+        y_chain = model(x)
+        model.chain_blocks = False
+        y_sep = model(x)
+    torch.cuda.synchronize()
+    assert rel_l2(y_chain, y_sep) < 2e-6
+
+
+def test_chain_argument_errors(device):
+    from nsw import ops
+    blocks, _ = make_stack(device, torch.float32, 1, 18, 36, 128, 2, (9, 18), ALT, seed=3)
+    x = torch.zeros(1, 1, 18, 36, 128, device=device)
+    packs = [b.packed(fold_all=True) for b in blocks]
+    with pytest.raises(ValueError):
+        ops.swin_blocks_forward(x, packs, 2, (9, 18), [(0, 0)])            # one shift for two blocks
+    bad = [dict(packs[0]), packs[1]]
+    del bad[0]["w1_n2"]
+    with pytest.raises(ValueError, match="norm-folded"):
+        ops.swin_blocks_forward(x, bad, 2, (9, 18), [(0, 0), (4, 9)])
+    with pytest.raises(ValueError, match="alias"):
+        ops.swin_blocks_forward(x, packs, 2, (9, 18), [(0, 0), (4, 9)], out=x)

@@ -30,7 +30,8 @@ def test_header_declares_the_abi():
     fns = declared_functions()
     for f in ["nsw_swin_block_forward", "nsw_window_attention", "nsw_linear", "nsw_qkv_projection",
               "nsw_rmsnorm_roll_partition", "nsw_proj_reverse_residual", "nsw_weighted_metrics",
-              "nsw_last_error", "nsw_block_workspace_size"]:
+              "nsw_last_error", "nsw_block_workspace_size", "nsw_swin_blocks_forward",
+              "nsw_blocks_workspace_size", "nsw_window_partition_sumsq"]:
         assert f in fns
 
 
@@ -84,6 +85,39 @@ def test_validation_errors_without_gpu(L):
     prm = _lib.BlockParams()
     rc = L.nsw_swin_block_forward(16, 16, ctypes.byref(prm), ctypes.byref(shp), 16, 1 << 30, None)
     assert rc == _lib.NSW_ERR_INVALID and b"alias" in L.nsw_last_error()
+
+
+def test_blocks_chain_validation_without_gpu(L):
+    """nsw_swin_blocks_forward refuses malformed stacks before any launch."""
+    from nsw import _lib
+    shapes = (_lib.BlockShape * 2)(_lib.BlockShape(1, 1, 18, 36, 128, 2, 9, 18, 0, 0, 512, 1e-7, 1),
+                                   _lib.BlockShape(1, 1, 18, 36, 128, 2, 9, 18, 4, 9, 512, 1e-7, 1))
+    params = (_lib.BlockParams * 2)()
+    for i in range(2):
+        params[i].wqkv_n1 = params[i].w1_n2 = 16
+    ws = 1 << 30
+    # depth 0
+    rc = L.nsw_swin_blocks_forward(16, 32, params, shapes, 0, 16, ws, None)
+    assert rc == _lib.NSW_ERR_INVALID and b"depth" in L.nsw_last_error()
+    # the folded weights are required
+    params[1].w1_n2 = None
+    rc = L.nsw_swin_blocks_forward(16, 32, params, shapes, 2, 16, ws, None)
+    assert rc == _lib.NSW_ERR_INVALID and b"norm-folded" in L.nsw_last_error()
+    params[1].w1_n2 = 16
+    # all blocks share one geometry (shift aside)
+    shapes[1].C = 256
+    rc = L.nsw_swin_blocks_forward(16, 32, params, shapes, 2, 16, ws, None)
+    assert rc == _lib.NSW_ERR_INVALID and b"differs" in L.nsw_last_error()
+    shapes[1].C = 128
+    # workspace too small
+    need = L.nsw_blocks_workspace_size(shapes, 2)
+    rc = L.nsw_swin_blocks_forward(16, 32, params, shapes, 2, 16, need - 1, None)
+    assert rc == _lib.NSW_ERR_INVALID and b"workspace" in L.nsw_last_error()
+    # two window-order row buffers, qkv/u, o, h1 and two sums-of-squares arrays
+    M, C, Hm, parts = 18 * 36, 128, 512, 1        # qkv and u share one buffer of max(3C, Hm) columns
+    assert need >= M * C * 2 * 4 + M * Hm * 2 + 2 * M * parts * 4
+    assert need < M * C * 2 * 4 + M * Hm * 2 + 2 * M * parts * 4 + 8 * 256
+    assert L.nsw_blocks_workspace_size(shapes, 0) == 0
 
 
 def test_fastdiv_selftest(L):
