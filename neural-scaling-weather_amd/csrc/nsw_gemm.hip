@@ -392,7 +392,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[nb][r] = gelu_erf(v[nb][r]);
+        for (int r = 0; r < 4; ++r) v[nb][r] = sizeof(T) == 2 ? gelu_erf_bf16(v[nb][r]) : gelu_erf(v[nb][r]);
     } else if constexpr (EPI == EPI_BIAS_GELU_TANH) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
