@@ -24,7 +24,10 @@
 
 namespace nsw {
 
-constexpr int MODEL_LDS = 64 * 1024;   // dynamic LDS per workgroup
+constexpr int MODEL_LDS = 64 * 1024;   // dynamic LDS per workgroup (at most)
+// unpatchify's tile: smaller tiles, more workgroups per CU (measured at
+// config 3: 24 KB tiles 70 us against 77 us with 64 KB)
+constexpr int UNPATCH_LDS = 24 * 1024;
 
 template <typename T> struct VecOf;
 template <> struct VecOf<bf16> { using V = bf16x8; };
@@ -74,25 +77,43 @@ __global__ __launch_bounds__(256) void im2col_kernel(const TX* __restrict__ x, c
     TO* trow = tile + r * KS;
     const int64_t xb = xbase[r];
     const int ib = ibase[r];
-    const int p_ = P > 0 ? P : p;
-#pragma unroll 4
-    for (int cu = grp; cu < C * p_; cu += groups) {
-      const int c = cu / p_, u = cu - c * p_;
-      const TX* src = c < Cx ? x + xb + c * HW + (int64_t)u * W : inv + (int64_t)(c - Cx) * HW + ib + u * W;
-      TO* dst = trow + cu * p_;
-      if constexpr (P > 0) {
-        // P consecutive elements, aligned to P * sizeof(T) (host-checked)
-        constexpr int SA = P * sizeof(TX) < 16 ? P * sizeof(TX) : 16;
-        constexpr int DA = P * sizeof(TO) < 16 ? P * sizeof(TO) : 16;
-        const TX* s_ = (const TX*)__builtin_assume_aligned(src, SA);
-        TO* d_ = (TO*)__builtin_assume_aligned(dst, DA);
-        TX v[P];
+    if constexpr (P > 0) {
+      // P consecutive elements per (c, u), aligned to P * sizeof(TX)
+      // (host-checked); U loads in flight per lane before their LDS stores
+      constexpr int SA = P * sizeof(TX) < 16 ? P * sizeof(TX) : 16;
+      constexpr int DA = P * sizeof(TO) < 16 ? P * sizeof(TO) : 16;
+      constexpr int UB = 128 / (P * (int)sizeof(TX));
+      constexpr int U = UB < 1 ? 1 : (UB > 16 ? 16 : UB);
+      const int total = C * P;
+      for (int cu0 = grp; cu0 < total; cu0 += U * groups) {
+        TX v[U][P];
 #pragma unroll
-        for (int e = 0; e < P; ++e) v[e] = s_[e];
+        for (int q = 0; q < U; ++q) {
+          const int cu = cu0 + q * groups;
+          if (cu < total) {
+            const int c = cu / P, u = cu - c * P;
+            const TX* src = c < Cx ? x + xb + c * HW + (int64_t)u * W : inv + (int64_t)(c - Cx) * HW + ib + u * W;
+            const TX* s_ = (const TX*)__builtin_assume_aligned(src, SA);
 #pragma unroll
-        for (int e = 0; e < P; ++e) d_[e] = from_f32<TO>(to_f32(v[e]));
-      } else {
-        for (int e = 0; e < p_; ++e) dst[e] = from_f32<TO>(to_f32(src[e]));
+            for (int e = 0; e < P; ++e) v[q][e] = s_[e];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < U; ++q) {
+          const int cu = cu0 + q * groups;
+          if (cu < total) {
+            TO* d_ = (TO*)__builtin_assume_aligned(trow + cu * P, DA);
+#pragma unroll
+            for (int e = 0; e < P; ++e) d_[e] = from_f32<TO>(to_f32(v[q][e]));
+          }
+        }
+      }
+    } else {
+      for (int cu = grp; cu < C * p; cu += groups) {
+        const int c = cu / p, u = cu - c * p;
+        const TX* src = c < Cx ? x + xb + c * HW + (int64_t)u * W : inv + (int64_t)(c - Cx) * HW + ib + u * W;
+        TO* dst = trow + cu * p;
+        for (int e = 0; e < p; ++e) dst[e] = from_f32<TO>(to_f32(src[e]));
       }
     }
   }
@@ -116,7 +137,7 @@ __global__ __launch_bounds__(256) void im2col_kernel(const TX* __restrict__ x, c
 
 template <typename TI, typename TO, int P>
 __global__ __launch_bounds__(256) void unpatchify_kernel(const TI* __restrict__ y, int Co, int H, int W, int p,
-                                                         int64_t out_bstride, int64_t M, int R,
+                                                         int64_t out_bstride, int64_t M, int R, int pairs,
                                                          TO* __restrict__ out) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   TI* tile = reinterpret_cast<TI*>(smem);
@@ -148,8 +169,70 @@ __global__ __launch_bounds__(256) void unpatchify_kernel(const TI* __restrict__ 
   }
   __syncthreads();
 
-  // scatter: one lane per tile row; per iteration a lane writes the p
-  // consecutive pixels of its patch in one output row (one vector store)
+  // scatter: per iteration a lane writes the p consecutive pixels of its
+  // patch in one output row (one vector store), or, with `pairs` (host:
+  // even R and w, output aligned), the 2p pixels of two horizontally
+  // adjacent patches (tile rows 2k, 2k + 1 of one image row)
+  if constexpr (P > 0) {
+    if (pairs) {
+      const int RP = R / 2, rowsP = rows / 2;    // rows is even with pairs
+      const int groups = 256 / RP;
+      const int rp = tid % RP, grp = tid / RP;
+      if (rp < rowsP && grp < groups) {
+        constexpr int DA = 2 * P * sizeof(TO) < 16 ? 2 * P * sizeof(TO) : 16;
+        const TI* t0 = tile + 2 * rp * NS;
+        const TI* t1 = t0 + NS;
+        const int64_t ob = obase[2 * rp];
+        bool done = false;
+        if constexpr (sizeof(TI) == 2) {
+          if (Co % 2 == 0) {
+          done = true;
+          // two channels per lane: each LDS read (4 bytes) serves two planes
+          const int Ch = Co / 2;
+#pragma unroll 2
+          for (int cu = grp; cu < Ch * P; cu += groups) {
+            const int c = 2 * (cu / P), u = cu - (cu / P) * P;
+            const int so = u * P * Co + c;
+            TO v0[2 * P], v1[2 * P];
+#pragma unroll
+            for (int e = 0; e < P; ++e) {
+              const uint32_t a = *reinterpret_cast<const uint32_t*>(t0 + so + e * Co);
+              const uint32_t b = *reinterpret_cast<const uint32_t*>(t1 + so + e * Co);
+              const bf16x2 pa = __builtin_bit_cast(bf16x2, a), pb = __builtin_bit_cast(bf16x2, b);
+              v0[e] = from_f32<TO>((float)pa[0]);
+              v1[e] = from_f32<TO>((float)pa[1]);
+              v0[P + e] = from_f32<TO>((float)pb[0]);
+              v1[P + e] = from_f32<TO>((float)pb[1]);
+            }
+            TO* d0 = (TO*)__builtin_assume_aligned(out + ob + c * HW + (int64_t)u * W, DA);
+            TO* d1 = (TO*)__builtin_assume_aligned(out + ob + (c + 1) * HW + (int64_t)u * W, DA);
+#pragma unroll
+            for (int e = 0; e < 2 * P; ++e) d0[e] = v0[e];
+#pragma unroll
+            for (int e = 0; e < 2 * P; ++e) d1[e] = v1[e];
+          }
+          }
+        }
+        if (!done) {
+#pragma unroll 2
+          for (int cu = grp; cu < Co * P; cu += groups) {
+            const int c = cu / P, u = cu - c * P;
+            TO* d_ = (TO*)__builtin_assume_aligned(out + ob + c * HW + (int64_t)u * W, DA);
+            const int so = u * P * Co + c;
+            TO v[2 * P];
+#pragma unroll
+            for (int e = 0; e < P; ++e) {
+              v[e] = from_f32<TO>(to_f32(t0[so + e * Co]));
+              v[P + e] = from_f32<TO>(to_f32(t1[so + e * Co]));
+            }
+#pragma unroll
+            for (int e = 0; e < 2 * P; ++e) d_[e] = v[e];
+          }
+        }
+      }
+      return;
+    }
+  }
   const int groups = 256 / R;
   const int r = tid % R, grp = tid / R;
   if (r < rows && grp < groups) {
@@ -177,11 +260,10 @@ __global__ __launch_bounds__(256) void unpatchify_kernel(const TI* __restrict__ 
 }
 
 // Rows per workgroup: at most 64 (four lane groups split the (c, u) pairs)
-// and at most MODEL_LDS of tile.
-static int rows_per_wg(int p, int row_bytes) {
-  (void)p;
+// and at most `budget` bytes of tile (at least one row).
+static int rows_per_wg(int budget, int row_bytes) {
   int r = 64;
-  const int lim = MODEL_LDS / row_bytes;
+  const int lim = budget / row_bytes;
   if (lim < r) r = lim;
   return r < 1 ? 1 : r;
 }
@@ -210,7 +292,7 @@ extern "C" int nsw_patch_im2col(const void* x, const void* inv, int64_t B, int64
   const size_t es = dtype_size(out_dtype);
   const int row_bytes = (int)((Kp + V) * es);
   NSW_CHECK_ARG(row_bytes <= MODEL_LDS, "%s: Kp=%lld too large for one LDS row", what, (long long)Kp);
-  const int R = rows_per_wg((int)p, row_bytes);
+  const int R = rows_per_wg(MODEL_LDS, row_bytes);
   const int64_t grid = (M + R - 1) / R;
   NSW_CHECK_ARG(grid < (1LL << 31), "%s: too many rows", what);
   hipStream_t st = (hipStream_t)stream;
@@ -259,7 +341,9 @@ extern "C" int nsw_unpatchify(const void* y, void* out, int64_t B, int64_t C_out
   const size_t es = dtype_size(in_dtype);
   const int row_bytes = (int)((N + V) * es);
   NSW_CHECK_ARG(row_bytes <= MODEL_LDS, "%s: p*p*C_out=%lld too large for one LDS row", what, (long long)N);
-  const int R = rows_per_wg((int)p, row_bytes);
+  int R = rows_per_wg(UNPATCH_LDS, row_bytes);
+  const int64_t wp = W / p;
+  if (R > 1) R &= ~1;                            // even: tile rows pair up inside image rows when wp is even
   const int64_t grid = (M + R - 1) / R;
   NSW_CHECK_ARG(grid < (1LL << 31), "%s: too many rows", what);
   hipStream_t st = (hipStream_t)stream;
@@ -269,9 +353,12 @@ extern "C" int nsw_unpatchify(const void* y, void* out, int64_t B, int64_t C_out
   const bool vec = (p == 1 || p == 2 || p == 4 || p == 8 || p == 16) &&
                    ((uintptr_t)out % std::min<size_t>(16, p * oes)) == 0 &&
                    ((out_bstride * (int64_t)oes) % (int64_t)std::min<size_t>(16, p * oes)) == 0;
+  const size_t pa = std::min<size_t>(16, 2 * p * oes);
+  const int pairs = vec && R % 2 == 0 && wp % 2 == 0 && ((uintptr_t)out % pa) == 0 &&
+                    ((out_bstride * (int64_t)oes) % (int64_t)pa) == 0 && ((H * W * (int64_t)oes) % (int64_t)pa) == 0;
 #define NSW_UNPATCH_P(TI, TO, P)                                                                           \
   hipLaunchKernelGGL((unpatchify_kernel<TI, TO, P>), g, blk, shm, st, (const TI*)y, (int)C_out, (int)H,    \
-                     (int)W, (int)p, out_bstride, M, R, (TO*)out)
+                     (int)W, (int)p, out_bstride, M, R, pairs, (TO*)out)
 #define NSW_UNPATCH(TI, TO)                                                                                \
   do {                                                                                                     \
     if (!vec) NSW_UNPATCH_P(TI, TO, 0);                                                                    \

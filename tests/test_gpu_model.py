@@ -59,7 +59,9 @@ def test_patch_im2col_bit_exact(device, xd, od, B, T, Cx, Ci, H, W, p, frame0):
 
 @pytest.mark.parametrize("idt,odt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
                                      (torch.float32, torch.float32)])
-@pytest.mark.parametrize("B,Co,H,W,p", [(1, 70, 32, 64, 4), (2, 6, 12, 16, 2), (3, 4, 9, 6, 3)])
+@pytest.mark.parametrize("B,Co,H,W,p", [(1, 70, 32, 64, 4), (2, 6, 12, 16, 2), (3, 4, 9, 6, 3),
+                                         (1, 8, 8, 20, 4),      # odd patches per row: one patch per lane
+                                         (2, 70, 36, 40, 4)])   # two patches per lane, many workgroups
 def test_unpatchify_bit_exact(device, idt, odt, B, Co, H, W, p):
     import nsw
     h, w = H // p, W // p
