@@ -18,7 +18,9 @@ The line also carries
 and, unless --no-model is given,
   "forecast": config 3, one SwinTransformer forward (p4, e1024, depth 16,
               16 heads, window 9x18, 70 channels, 720x1440, bf16) = ms per
-              forecast step, split into embedding / blocks / head;
+              forecast step, split into embedding / blocks / head (the
+              blocks as one window-order chain), and the same step with one
+              fused call per block (ms_per_step_block_calls);
   "rollout":  config 5, 8 autoregressive steps of the config-3 model with
               per-step latitude-weighted RMSE and ACC (nsw.Rollout), bf16
               against the same weights in fp32: per-step drift.
@@ -104,6 +106,9 @@ def main():
                          "markdown and write profiles/traffic_<config>.json")
     ap.add_argument("--no-config4", action="store_true", help="skip the config-4 block and model timing")
     ap.add_argument("--no-gemm-compare", action="store_true", help="skip the hipBLASLt comparison leg")
+    ap.add_argument("--no-block-calls", action="store_true",
+                    help="skip the config-3 comparison run with one fused call per block (the forward keeps "
+                         "the residual stream in window order between blocks)")
     args = ap.parse_args()
 
     if args.traffic_summary:
@@ -288,7 +293,8 @@ def main():
     if not args.no_model:
         del y, y2
         torch.cuda.empty_cache()
-        out["forecast"], rollout = model_sections(dev, args.model_steps, args.warmup, not args.no_rollout)
+        out["forecast"], rollout = model_sections(dev, args.model_steps, args.warmup, not args.no_rollout,
+                                                  not args.no_block_calls)
         if rollout is not None:
             out["rollout"] = rollout
 
@@ -505,7 +511,7 @@ def smooth_fields(shape, sigma, seed, dev):
     return x
 
 
-def model_sections(dev, steps, warmup, with_rollout=True):
+def model_sections(dev, steps, warmup, with_rollout=True, with_block_calls=True):
     """Config 3 (one forecast step of the d16 model) and config 5 (8-step
     rollout, bf16 vs fp32)."""
     import numpy as np
@@ -549,16 +555,18 @@ def model_sections(dev, steps, warmup, with_rollout=True):
         if not torch.isfinite(yb.float()).all():
             raise RuntimeError("non-finite forecast")
         # the same step with one fused call per block (no window-order chain)
-        model.chain_blocks = False
-        for _ in range(2):
-            model(x)
-        e0.record(stream)
-        for _ in range(steps):
-            model(x)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms_per_block = e0.elapsed_time(e1) / steps
-        model.chain_blocks = True
+        ms_per_block = None
+        if with_block_calls:
+            model.chain_blocks = False
+            for _ in range(2):
+                model(x)
+            e0.record(stream)
+            for _ in range(steps):
+                model(x)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms_per_block = e0.elapsed_time(e1) / steps
+            model.chain_blocks = True
     forecast = {
         "workload": "config 3: SwinTransformer fwd, [1,1,70,720,1440] -> [1,1,70,720,1440], p4 e1024 depth 16, "
                     "16 heads, window 9x18, alternating shift 0 / 4x9, coordinate pos-embed, bf16",
@@ -567,7 +575,7 @@ def model_sections(dev, steps, warmup, with_rollout=True):
         "tokens_per_s": round(tokens / (ms * 1e-3), 1),
         "embed_ms": round(ev[0].elapsed_time(ev[1]), 3), "blocks_ms": round(ev[1].elapsed_time(ev[2]), 3),
         "head_ms": round(ev[2].elapsed_time(ev[3]), 3),
-        "ms_per_step_block_calls": round(ms_per_block, 3),
+        "ms_per_step_block_calls": None if ms_per_block is None else round(ms_per_block, 3),
     }
     del tok, yb
     if not with_rollout:
