@@ -13,7 +13,7 @@ import math
 import torch
 from torch import nn
 
-from . import ops
+from . import ops, torch_ops
 
 _DEFAULT_META = {"sharded": [None, None], "shared": [], "reduce": []}
 
@@ -43,7 +43,7 @@ class LinearLayer(nn.Module):
         trunc_normal_(self.weight, std=0.02)
 
     def forward(self, x):
-        return ops.linear(x.contiguous(), self.weight)
+        return torch_ops.linear_epi(x, self.weight)
 
 
 class BiasLayer(nn.Module):
@@ -86,8 +86,9 @@ class NormLayer(nn.Module):
             n = self.norm
             if len(n.normalized_shape) != 1:
                 raise NotImplementedError("libnsw normalises over the last dim only")
-            return ops.layer_norm(x.contiguous(), n.weight, n.bias, n.eps)
+            return torch.ops.nsw.layer_norm(x, n.weight, n.bias, float(n.eps))
         w = self.norm.weight
         if w is None:
             w = torch.ones(x.shape[-1], dtype=x.dtype, device=x.device)
-        return ops.rms_norm(x.contiguous(), w, self.norm.eps)
+        eps = self.norm.eps
+        return torch.ops.nsw.rms_norm(x, w, ops.default_eps(x.dtype) if eps is None else float(eps))

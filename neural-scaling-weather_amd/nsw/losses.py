@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import ops
+from . import torch_ops  # noqa: F401  (registers torch.ops.nsw.*)
 
 
 def _reduce_leading(v: torch.Tensor, temporal_average: bool) -> torch.Tensor:
@@ -39,7 +39,7 @@ class WeightedRMSE(nn.Module):
 
     def forward(self, pred: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
         w = self.weights
-        rmse, _ = ops.weighted_metrics(pred.contiguous(), target.contiguous(), w)
+        rmse, _ = torch.ops.nsw.weighted_metrics(pred, target, w, None)
         return _reduce_leading(rmse.to(_out_dtype(w, pred)), self.temporal_average)
 
 
@@ -56,15 +56,14 @@ class WeightedACC(nn.Module):
         self.register_buffer("climatology", climatology)
 
     def forward(self, pred: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
-        _, acc = ops.weighted_metrics(pred.contiguous(), target.contiguous(), self.weights,
-                                      self.climatology)
+        _, acc = torch.ops.nsw.weighted_metrics(pred, target, self.weights, self.climatology)
         return _reduce_leading(acc.to(_out_dtype(self.weights, pred)), self.temporal_average)
 
 
 def weighted_rmse_acc(pred, target, weights, climatology=None, temporal_average: bool = True):
     """Both metrics from one pass over the fields."""
-    rmse, acc = ops.weighted_metrics(pred.contiguous(), target.contiguous(), weights, climatology)
+    rmse, acc = torch.ops.nsw.weighted_metrics(pred, target, weights, climatology)
     dt = _out_dtype(weights, pred)
     r = _reduce_leading(rmse.to(dt), temporal_average)
-    a = None if acc is None else _reduce_leading(acc.to(dt), temporal_average)
+    a = None if climatology is None else _reduce_leading(acc.to(dt), temporal_average)
     return r, a

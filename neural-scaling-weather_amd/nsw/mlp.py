@@ -12,7 +12,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from . import _lib, ops
+from . import _lib, torch_ops
 from .layer_helpers import BiasLayer, LinearLayer
 
 
@@ -52,8 +52,8 @@ class MLP(nn.Module):
         (models/swin_helpers.py:456)."""
         self._check_fusable()
         x = x.contiguous()
-        h = ops.linear(x, self.fc1.weight, self.bias1.bias, epilogue=self.gelu_epilogue)
+        h = torch_ops.linear_epi(x, self.fc1.weight, self.bias1.bias, epilogue=self.gelu_epilogue)
         if residual is None:
-            return ops.linear(h, self.fc2.weight, self.bias2.bias, epilogue=_lib.NSW_EPI_BIAS)
-        return ops.linear(h, self.fc2.weight, self.bias2.bias, residual=residual.contiguous(),
-                          epilogue=_lib.NSW_EPI_BIAS_RESIDUAL)
+            return torch_ops.linear_epi(h, self.fc2.weight, self.bias2.bias, epilogue=_lib.NSW_EPI_BIAS)
+        return torch_ops.linear_epi(h, self.fc2.weight, self.bias2.bias, residual=residual,
+                                    epilogue=_lib.NSW_EPI_BIAS_RESIDUAL)

@@ -25,7 +25,7 @@ from typing import Optional
 import torch
 from torch import nn
 
-from . import ops
+from . import ops, torch_ops
 from .layer_helpers import LinearLayer, trunc_normal_
 from .swin_helpers import Block as BlockDefault
 
@@ -65,19 +65,24 @@ class Conv2DLayer(nn.Module):
         (c, u, v) order, zero columns up to the GEMM k granularity), cached
         until the parameters change."""
         w, b = self.conv.weight, self.conv.bias
+        if torch.compiler.is_compiling():     # traced: built each call (the cache key reads data_ptr)
+            return self._build_pack()
         key = (w.data_ptr(), w._version, w.dtype, w.device,
                None if b is None else (b.data_ptr(), b._version))
         if self._pack_key != key:
-            E = w.shape[0]
-            K = w[0].numel()
-            g = ops.k_granule(w.dtype)
-            Kp = (K + g - 1) // g * g
-            wp = torch.zeros(E, Kp, dtype=w.dtype, device=w.device)
             with torch.no_grad():
-                wp[:, :K].copy_(w.detach().reshape(E, K))
-            self._pack = (wp, None if b is None else b.detach().contiguous(), Kp)
+                self._pack = self._build_pack()
             self._pack_key = key
         return self._pack
+
+    def _build_pack(self):
+        w, b = self.conv.weight, self.conv.bias
+        E = w.shape[0]
+        K = w[0].numel()
+        g = ops.k_granule(w.dtype)
+        Kp = (K + g - 1) // g * g
+        wp = torch.nn.functional.pad(w.detach().reshape(E, K), (0, Kp - K)).contiguous()
+        return wp, None if b is None else b.detach().contiguous(), Kp
 
     def tokens(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
                invariants: Optional[torch.Tensor] = None, frame0: int = 0) -> torch.Tensor:
@@ -86,13 +91,13 @@ class Conv2DLayer(nn.Module):
         B, T, C, H, W = x.shape
         p = self.patch
         wp, b, Kp = self.packed()
-        pm = ops.patch_im2col(x.contiguous(), p, Kp, wp.dtype, invariants=invariants, frame0=frame0)
+        pm = torch.ops.nsw.patch_im2col(x, p, Kp, wp.dtype, invariants, int(frame0))
         if b is None:
             if residual is not None:
                 raise NotImplementedError("a residual without a conv bias is not fused")
-            y = ops.linear(pm, wp)
+            y = torch_ops.linear_epi(pm, wp)
         else:
-            y = ops.linear(pm, wp, b, residual=residual)
+            y = torch_ops.linear_epi(pm, wp, b, residual=residual)
         return y.view(B, T, H // p, W // p, wp.shape[0])
 
     def forward(self, x):
@@ -254,7 +259,10 @@ class SwinTransformer(nn.Module):
     # ------------------------------------------------------------ embedding --
     def _pos_tokens(self, B: int, dtype: torch.dtype, device) -> torch.Tensor:
         """Positional embedding in token layout, repeated over the batch:
-        [B*T*h*w, E] (the GEMM epilogue's residual operand)."""
+        [B*T*h*w, E] (the GEMM epilogue's residual operand); cached until the
+        parameters change, rebuilt each call while torch.compile traces."""
+        if torch.compiler.is_compiling():
+            return self._build_pos(B, dtype, device)
         if self.coord_pos_embed:
             w, b = self.pos_embed.proj.conv.weight, self.pos_embed.proj.conv.bias
             key = ("coord", w.data_ptr(), w._version, b.data_ptr(), b._version, self.coords.data_ptr(),
@@ -263,16 +271,19 @@ class SwinTransformer(nn.Module):
             key = ("param", self.pos_embed.data_ptr(), self.pos_embed._version, dtype, torch.device(device), B)
         if self._pos_key != key:
             with torch.no_grad():
-                if self.coord_pos_embed:
-                    c = self.coords.to(device=device, dtype=self.pos_embed.proj.conv.weight.dtype)
-                    c = c.permute(0, 3, 1, 2).contiguous().unsqueeze(0)       # [1, T, 4, H, W]
-                    pos = self.pos_embed.tokens(c)                             # [1, T, h, w, E]
-                else:
-                    pos = self.pos_embed.detach()
-                pos = pos.to(device=device, dtype=dtype).expand(B, -1, -1, -1, -1)
-                self._pos = pos.reshape(-1, self.embed_dim).contiguous()
+                self._pos = self._build_pos(B, dtype, device)
             self._pos_key = key
         return self._pos
+
+    def _build_pos(self, B: int, dtype: torch.dtype, device) -> torch.Tensor:
+        if self.coord_pos_embed:
+            c = self.coords.to(device=device, dtype=self.pos_embed.proj.conv.weight.dtype)
+            c = c.permute(0, 3, 1, 2).contiguous().unsqueeze(0)       # [1, T, 4, H, W]
+            pos = self.pos_embed.tokens(c)                             # [1, T, h, w, E]
+        else:
+            pos = self.pos_embed.detach()
+        pos = pos.to(device=device, dtype=dtype).expand(B, -1, -1, -1, -1)
+        return pos.reshape(-1, self.embed_dim).contiguous()
 
     def prepare_tokens(self, x: torch.Tensor, invariants: Optional[torch.Tensor] = None,
                        frame0: int = 0) -> torch.Tensor:
@@ -286,8 +297,8 @@ class SwinTransformer(nn.Module):
         """models/swin.py:286-299: [B, T, h, w, E] -> [B, T, C_out, H, W]."""
         b, t, h, w, c = x.shape
         p = self.patch_size
-        y = ops.linear(x.contiguous().view(-1, c), self.head.weight)
-        out = ops.unpatchify(y, b * t, self.out_chans, h * p, w * p, p)
+        y = torch_ops.linear_epi(x.reshape(-1, c), self.head.weight)
+        out = torch.ops.nsw.unpatchify(y, b * t, self.out_chans, h * p, w * p, p, None)
         return out.view(b, t, self.out_chans, h * p, w * p)
 
     def _head_last(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -296,6 +307,9 @@ class SwinTransformer(nn.Module):
         b, t, h, w, c = x.shape
         p = self.patch_size
         W = self.head.weight
+        if out is None:
+            y = torch_ops.linear_epi(x[:, t - 1].reshape(b * h * w, c), W)
+            return torch.ops.nsw.unpatchify(y, b, self.out_chans, h * p, w * p, p, None)
         y = torch.empty(b * h * w, self.out_size, dtype=x.dtype, device=x.device)
         for bi in range(b):
             ops.linear(x[bi, t - 1].view(h * w, c), W, out=y[bi * h * w:(bi + 1) * h * w])
@@ -328,10 +342,12 @@ class SwinTransformer(nn.Module):
         tanh = {blk.mlp.gelu_tanh for blk in self.blocks}
         if len(eps) != 1 or len(tanh) != 1:
             raise NotImplementedError("the block chain needs one eps and one GELU form for all blocks")
-        packs = [blk.packed(fold_all=True) for blk in self.blocks]
-        shifts = [blk.shift_size for blk in self.blocks]
-        return ops.swin_blocks_forward(y.contiguous(), packs, b0.num_heads, b0.window_size, shifts,
-                                       eps=eps.pop(), gelu_tanh=tanh.pop())
+        params, shifts = [], []
+        for blk in self.blocks:
+            params += torch_ops.block_param_list(blk.packed(fold_all=True))
+            shifts += [int(blk.shift_size[0]), int(blk.shift_size[1])]
+        return torch.ops.nsw.swin_blocks(y, params, b0.num_heads, [int(v) for v in b0.window_size], shifts,
+                                         eps.pop(), tanh.pop())
 
 
 class TimeStepper(nn.Module):

@@ -20,20 +20,20 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 
-from . import _lib, ops
+from . import _lib, ops, torch_ops
 from .layer_helpers import BiasLayer, LinearLayer, NormLayer
 from .mlp import MLP
 
 
 def window_partition(x: torch.Tensor, window_size: Tuple[int, int]) -> torch.Tensor:
     """models/swin_helpers.py:26-51: [B,T,H,W,C] -> [B*nW, T, ws0, ws1, C]."""
-    return ops.window_partition(x.contiguous(), tuple(window_size))
+    return torch.ops.nsw.window_partition(x, [int(w) for w in window_size])
 
 
 def window_reverse(windows: torch.Tensor, window_size: Tuple[int, int],
                    img_size: Tuple[int, int]) -> torch.Tensor:
     """models/swin_helpers.py:54-77: [B*nW, T, ws0, ws1, C] -> [B,T,H,W,C]."""
-    return ops.window_reverse(windows.contiguous(), tuple(window_size), tuple(img_size))
+    return torch.ops.nsw.window_reverse(windows, [int(w) for w in window_size], [int(v) for v in img_size])
 
 
 def roll_forward_reverseroll_backward(x, shifts, dims, comm_names=None):
@@ -43,7 +43,7 @@ def roll_forward_reverseroll_backward(x, shifts, dims, comm_names=None):
         raise NotImplementedError("libnsw rolls the (H, W) dims of a [B,T,H,W,C] tensor")
     if not any(shifts):
         return x
-    return ops.roll_hw(x.contiguous(), tuple(shifts))
+    return torch.ops.nsw.roll_hw(x, [int(v) for v in shifts])
 
 
 def attention_mask_closed_form(H: int, W: int, window_size: Tuple[int, int], shift_size: Tuple[int, int],
@@ -108,8 +108,12 @@ class WindowMultiHeadAttention(nn.Module):
         self._pack = None
 
     def packed_qkv(self):
-        """[Wq;Wk;Wv] and [bq;bk;bv], rebuilt when a parameter changes."""
+        """[Wq;Wk;Wv] and [bq;bk;bv], rebuilt when a parameter changes (not
+        cached while torch.compile traces: the cache key reads data_ptr)."""
         ps = (self.q.weight, self.k.weight, self.v.weight, self.biasq.bias, self.biask.bias, self.biasv.bias)
+        if torch.compiler.is_compiling():
+            return (torch.cat([p.detach() for p in ps[:3]], 0).contiguous(),
+                    torch.cat([p.detach() for p in ps[3:]], 0).contiguous())
         key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in ps)
         if key != self._pack_key:
             with torch.no_grad():
@@ -137,10 +141,13 @@ class WindowMultiHeadAttention(nn.Module):
         eps = _eps_of(self.q_norm, x.dtype)
         if eps != _eps_of(self.k_norm, x.dtype):
             raise NotImplementedError("q_norm and k_norm must share eps")
-        qkv = ops.qkv_projection(x.contiguous(), wqkv, bqkv, qn, kn, self.num_heads, eps)
-        o = ops.window_attention(qkv, self.num_heads, self.scale, mask=mask,
-                                 geometry=geometry if mask is None else None)
-        return ops.linear(o, self.proj.weight, self.biasproj.bias)
+        qkv = torch.ops.nsw.qkv_projection(x, wqkv, bqkv, qn, kn, self.num_heads, float(eps))
+        geo = []
+        if mask is None and geometry is not None:
+            H, W, ws, sh, T = geometry
+            geo = [int(H), int(W), int(ws[0]), int(ws[1]), int(sh[0]), int(sh[1]), int(T)]
+        o = torch.ops.nsw.window_attention(qkv, self.num_heads, float(self.scale), mask, geo)
+        return torch_ops.linear_epi(o, self.proj.weight, self.biasproj.bias)
 
 
 class Block(nn.Module):
@@ -202,33 +209,48 @@ class Block(nn.Module):
         weights are included as fold_norm1 / fold_norm2 ask, or both when
         ``fold_all`` (the window-order chain of SwinTransformer.forward)."""
         a = self.attn
+        fold1, fold2 = self.fold_norm1 or fold_all, self.fold_norm2 or fold_all
+        if torch.compiler.is_compiling():
+            # traced: built from the parameters each call (the cache key reads data_ptr)
+            return self._build_pack(fold1, fold2)
         ps = [self.norm1.norm.weight, a.q.weight, a.k.weight, a.v.weight, a.biasq.bias, a.biask.bias,
               a.biasv.bias, a.q_norm.norm.weight, a.k_norm.norm.weight, a.proj.weight, a.biasproj.bias,
               self.norm2.norm.weight, self.mlp.fc1.weight, self.mlp.bias1.bias, self.mlp.fc2.weight,
               self.mlp.bias2.bias]
         key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in ps)
         if key != self._pack_key:
-            wqkv, bqkv = a.packed_qkv()
-            d = lambda t: t.detach().contiguous()
-            self._pack = {
-                "norm1_w": d(self.norm1.norm.weight), "wqkv": wqkv, "bqkv": bqkv,
-                "qn_w": d(a.q_norm.norm.weight), "kn_w": d(a.k_norm.norm.weight),
-                "wproj": d(a.proj.weight), "bproj": d(a.biasproj.bias),
-                "norm2_w": d(self.norm2.norm.weight), "w1": d(self.mlp.fc1.weight),
-                "b1": d(self.mlp.bias1.bias), "w2": d(self.mlp.fc2.weight), "b2": d(self.mlp.bias2.bias),
-            }
+            self._pack = self._build_pack(False, False)
             self._pack_key = key
         pk = self._pack
         with torch.no_grad():
-            # norm weights folded into the GEMM weights that consume the
-            # normalised rows: RMSNorm(x) . W^T = rs(x) * (x . (W * norm_w)^T)
-            if (self.fold_norm1 or fold_all) and "wqkv_n1" not in pk:
-                n1 = pk["norm1_w"].float()
-                pk["wqkv_n1"] = (pk["wqkv"].float() * n1[None, :]).to(pk["wqkv"].dtype).contiguous()
-            if (self.fold_norm2 or fold_all) and "w1_n2" not in pk:
-                n2 = pk["norm2_w"].float()
-                pk["w1_n2"] = (pk["w1"].float() * n2[None, :]).to(pk["w1"].dtype).contiguous()
+            if fold1 and "wqkv_n1" not in pk:
+                pk["wqkv_n1"] = self._fold(pk["wqkv"], pk["norm1_w"])
+            if fold2 and "w1_n2" not in pk:
+                pk["w1_n2"] = self._fold(pk["w1"], pk["norm2_w"])
         return self._pack
+
+    @staticmethod
+    def _fold(w: torch.Tensor, norm_w: torch.Tensor) -> torch.Tensor:
+        """Norm weight folded into the GEMM weight that consumes the normalised
+        rows: RMSNorm(x) . W^T = rs(x) * (x . (W * norm_w)^T), per input column."""
+        return (w.float() * norm_w.float()[None, :]).to(w.dtype).contiguous()
+
+    def _build_pack(self, fold1: bool, fold2: bool) -> dict:
+        a = self.attn
+        wqkv, bqkv = a.packed_qkv()
+        d = lambda t: t.detach().contiguous()
+        pk = {
+            "norm1_w": d(self.norm1.norm.weight), "wqkv": wqkv, "bqkv": bqkv,
+            "qn_w": d(a.q_norm.norm.weight), "kn_w": d(a.k_norm.norm.weight),
+            "wproj": d(a.proj.weight), "bproj": d(a.biasproj.bias),
+            "norm2_w": d(self.norm2.norm.weight), "w1": d(self.mlp.fc1.weight),
+            "b1": d(self.mlp.bias1.bias), "w2": d(self.mlp.fc2.weight), "b2": d(self.mlp.bias2.bias),
+        }
+        if fold1:
+            pk["wqkv_n1"] = self._fold(pk["wqkv"], pk["norm1_w"])
+        if fold2:
+            pk["w1_n2"] = self._fold(pk["w1"], pk["norm2_w"])
+        return pk
 
     def check_input(self, x: torch.Tensor) -> None:
         if x.dim() != 5 or tuple(x.shape[2:4]) != self.feat_size:
@@ -240,11 +262,12 @@ class Block(nn.Module):
     def _shifted_window_attn(self, x: torch.Tensor) -> torch.Tensor:
         """models/swin_helpers.py:399-433 on an already-normalised x."""
         B, T, H, W, C = x.shape
-        xw = ops.roll_window_partition(x.contiguous(), self.window_size, self.shift_size)
+        ws, sh = [int(v) for v in self.window_size], [int(v) for v in self.shift_size]
+        xw = torch.ops.nsw.roll_window_partition(x, ws, sh)
         xw = xw.view(-1, T * self.window_area, C)
         o = self.attn(xw, geometry=(H, W, self.window_size, self.shift_size, T))
-        return ops.window_reverse_roll(o.view(-1, T, self.window_size[0], self.window_size[1], C),
-                                       self.window_size, (H, W), self.shift_size)
+        return torch.ops.nsw.window_reverse_roll(o.view(-1, T, self.window_size[0], self.window_size[1], C),
+                                                 ws, [H, W], sh)
 
     def forward(self, x: torch.Tensor, condition: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x [B, T, H, W, C] -> [B, T, H, W, C] (models/swin_helpers.py:435-459)."""
@@ -253,8 +276,9 @@ class Block(nn.Module):
         drop = ([] if self.fold_norm1 else ["wqkv_n1"]) + ([] if self.fold_norm2 else ["w1_n2"])
         if drop:
             pk = {k: v for k, v in pk.items() if k not in drop}
-        return ops.swin_block_forward(x.contiguous(), pk, self.num_heads, self.window_size,
-                                      self.shift_size, eps=self._eps(x.dtype), gelu_tanh=self.mlp.gelu_tanh)
+        return torch.ops.nsw.swin_block(x, torch_ops.block_param_list(pk), self.num_heads,
+                                        [int(v) for v in self.window_size], [int(v) for v in self.shift_size],
+                                        self._eps(x.dtype), self.mlp.gelu_tanh)
 
 
 # Names used by north_star / other Swin code bases.
