@@ -140,16 +140,6 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
-// Sum over the 32 lanes [32h, 32h + 32) of a wavefront, valid on lanes 0 and
-// 32: each 16-lane row sum (row16_sum) plus that of the odd row next to it,
-// read with v_readlane (even row first).
-__device__ __forceinline__ float half32_sum_lead(float x, int lane) {
-  const float r = row16_sum(x);
-  const float o1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), 16));
-  const float o3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), 48));
-  return r + (lane & 32 ? o3 : o1);
-}
-
 __device__ __forceinline__ float rows4_max(float x) {
   float a = x, b = x;
   permlane16_swap(a, b);

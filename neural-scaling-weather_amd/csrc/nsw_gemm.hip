@@ -469,6 +469,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
     const int prow0 = pass * S::ROWS;                 // first tile row of this pass
     int orow[2][BATCH];                               // output row (token for the scatter) per batch row
     u32x4 rres[2][RES ? BATCH : 1];
+    float ssacc = 0.f;                                // row sums of squares of the pass (SUMSQ)
     // Row maps: the wave copies ITER * RPI (<= 64) consecutive rows per pass,
     // so lane l maps the wave's row l once and every copy instruction takes
     // its rows' targets from those lanes (v_readlane) instead of all 32 or
@@ -564,14 +565,34 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
           if (ok) *reinterpret_cast<u32x4*>(Y + (int64_t)orow[cur][b] * N + n) = ov[b];
         }
         if constexpr (SUMSQ) {
-          // partial sum of squares over 32 lanes (32 * VEC columns: two DPP
-          // rows, even row first), one float per 512 bytes of output row
+          // partial sum of squares over 32 lanes (32 * VEC columns, one float
+          // per 512 bytes of output row): the two 16-lane row sums of each
+          // half wave, even row first, parked in lane q * RPI + half (bf16:
+          // the half's tile row; fp32: row q, half = part) of ssacc, which
+          // is stored once per pass
           if (!SCAT || ea.row_sumsq != nullptr) {
-            ssq = half32_sum_lead(ssq, lane);
-            if ((lane & 31) == 0 && ok)
-              ea.row_sumsq[(int64_t)orow[cur][b] * ea.nparts + n / (32 * VEC)] = ssq;
+            const int ri = __builtin_bit_cast(int, row16_sum(ssq));
+            const float sa = __builtin_bit_cast(float, __builtin_amdgcn_readlane(ri, 0)) +
+                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(ri, 16));
+            const float sb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(ri, 32)) +
+                             __builtin_bit_cast(float, __builtin_amdgcn_readlane(ri, 48));
+            const int q = ib * BATCH + b;
+            constexpr int HB = RPI == 2 ? 1 : 32;       // lane offset of the upper half's value
+            ssacc = lane == q * RPI ? sa : ssacc;
+            ssacc = lane == q * RPI + HB ? sb : ssacc;
           }
         }
+      }
+    }
+    if constexpr (SUMSQ) {
+      // one store of the pass's row sums per wave: lane l holds wave row
+      // l % WROWS, part n0 / 256 (bf16) or n0 / 128 + l / 32 (fp32)
+      if (!SCAT || ea.row_sumsq != nullptr) {
+        const int rw = lane % WROWS;
+        const int m = m0 + prow0 + wave * WROWS + rw;
+        const int pcol = n0 + (RPI == 2 ? 0 : (lane / 32) * 32 * VEC);   // first column of the part
+        const int orw = MAPPED ? lmap : m;
+        if (m < M && pcol < N) ea.row_sumsq[(int64_t)orw * ea.nparts + pcol / (32 * VEC)] = ssacc;
       }
     }
     if (pass + 1 < S::PASSES) wg_barrier();          // before the next pass overwrites the staging rows
