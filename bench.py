@@ -91,10 +91,12 @@ def main():
     ap.add_argument("--no-model", action="store_true", help="skip the config-3 forecast and config-5 rollout")
     ap.add_argument("--model-steps", type=int, default=10, help="timed forecast steps (config 3)")
     ap.add_argument("--no-rollout", action="store_true", help="skip the config-5 rollout")
-    ap.add_argument("--norms", choices=["fold2", "fold12", "separate"], default="fold2",
-                    help="fold2 (default): norm2 folded into proj/fc1 via row sums of squares, 6 launches; "
-                         "fold12: norm1 also folded into the QKV GEMM, 5 launches (slower, an ablation); "
-                         "separate: both norms as passes of their own, 7 launches")
+    ap.add_argument("--norms", choices=["fold2", "window", "separate"], default="fold2",
+                    help="fold2 (default): norm1 as a gather pass, proj scattering to tokens with the norm2 "
+                         "sums, fc1 with norm2 as a row scale, 6 launches; window: both norms folded, the "
+                         "block as a one-block window-order chain (partition + norm1 sums, QKV with norm1 "
+                         "as a row scale, attention, proj with the norm2 sums, fc1, fc2 scattering to "
+                         "tokens), 6 launches; separate: both norms as passes of their own, 7 launches")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample time")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="before anything else, run a plain 256 MiB device copy (5 launches): the "
@@ -134,7 +136,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.manual_seed(1001)
     blk = nsw.Block(C, heads, (H, W), ws, T, shift_size=shift).to(device=dev, dtype=dtype).eval()
-    blk.fold_norm1 = args.norms == "fold12"
+    blk.fold_norm1 = args.norms == "window"
     blk.fold_norm2 = args.norms != "separate"
     g = torch.Generator().manual_seed(1002)
     x = torch.randn(B, T, H, W, C, generator=g).to(device=dev, dtype=dtype)
@@ -173,9 +175,23 @@ def main():
         def k_qkv():
             st["qkv"] = ops.qkv_projection(st["xw"], pk["wqkv"], pk["bqkv"], pk["qn_w"], pk["kn_w"], heads, eps)
 
-        def k_qkv_ng():
-            st["qkv"] = ops.qkv_projection_norm_gather(x, pk["wqkv_n1"], pk["bqkv"], pk["qn_w"], pk["kn_w"], heads,
-                                                       ws, shift, eps)
+        L = T * ws[0] * ws[1]
+
+        def k_part():
+            st["xw"], st["s1"] = ops.window_partition_sumsq(x, ws, shift)
+
+        def k_qkv_rs():
+            st["qkv"] = ops.qkv_projection_rowscale(st["xw"].view(-1, C), pk["wqkv_n1"], pk["bqkv"], pk["qn_w"],
+                                                    pk["kn_w"], st["s1"], heads, eps).view(-1, L, 3 * C)
+
+        def k_proj_id():
+            st["h1"], st["ss"] = ops.linear_remap_residual(st["o"].view(-1, C), pk["wproj"], pk["bproj"],
+                                                           st["xw"].view(-1, C), 0)
+
+        def k_fc2_tok():
+            y_, _ = ops.linear_remap_residual(st["u"], pk["w2"], pk["b2"], st["h1"], 1, image=(B, T, H, W),
+                                              window_size=ws, shift_size=shift)
+            st["y"] = y_.view(B, T, H, W, C)
 
         def k_attn():
             st["o"] = ops.window_attention(st["qkv"], heads, scale, geometry=(H, W, ws, shift, T))
@@ -199,11 +215,14 @@ def main():
         def k_fc2():
             st["y"] = ops.linear(st["u"], pk["w2"], pk["b2"], residual=st["h1"])
 
-        seq = ([("qkv_norm_gather", k_qkv_ng)] if blk.fold_norm1 else [("gather_norm1", k_gather), ("qkv", k_qkv)])
-        seq += [("attention", k_attn)]
-        seq += ([("proj_scatter_sumsq", k_proj_ss), ("fc1_rowscale", k_fc1_rs)] if blk.fold_norm2 else
-                [("proj_scatter", k_proj), ("norm2", k_norm2), ("fc1", k_fc1)])
-        seq += [("fc2", k_fc2)]
+        if args.norms == "window":
+            seq = [("partition_sumsq", k_part), ("qkv_rowscale", k_qkv_rs), ("attention", k_attn),
+                   ("proj_sumsq", k_proj_id), ("fc1_rowscale", k_fc1_rs), ("fc2_to_tokens", k_fc2_tok)]
+        else:
+            seq = [("gather_norm1", k_gather), ("qkv", k_qkv), ("attention", k_attn)]
+            seq += ([("proj_scatter_sumsq", k_proj_ss), ("fc1_rowscale", k_fc1_rs)] if blk.fold_norm2 else
+                    [("proj_scatter", k_proj), ("norm2", k_norm2), ("fc1", k_fc1)])
+            seq += [("fc2", k_fc2)]
         names = [n for n, _ in seq]
         times = {n: [] for n in names}
         for it in range(args.warmup + args.steps):
@@ -230,8 +249,9 @@ def main():
     work = {  # (algorithmic units per launch, bound)
         "gather_norm1": (2 * A, "hbm"), "qkv": (fl["qkv"], "mfma"), "attention": (4 * A, "hbm"),
         "proj_scatter": (fl["proj"], "mfma"), "norm2": (2 * A, "hbm"), "fc1": (fl["fc1"], "mfma"),
-        "fc2": (fl["fc2"], "mfma"), "qkv_norm_gather": (fl["qkv"], "mfma"), "fc1_rowscale": (fl["fc1"], "mfma"),
-        "proj_scatter_sumsq": (fl["proj"], "mfma"),
+        "fc2": (fl["fc2"], "mfma"), "fc1_rowscale": (fl["fc1"], "mfma"),
+        "proj_scatter_sumsq": (fl["proj"], "mfma"), "partition_sumsq": (2 * A, "hbm"),
+        "qkv_rowscale": (fl["qkv"], "mfma"), "proj_sumsq": (fl["proj"], "mfma"), "fc2_to_tokens": (fl["fc2"], "mfma"),
     }
     kern = {}
     for n in names:
@@ -321,10 +341,14 @@ def copy_calibration():
 
 
 # Kernel names in a rocprofv3 trace -> bench.py's kernel names (config 2,
-# bf16, the default 6-launch block).  The GEMM instances are told apart by
-# their (mangled) template arguments: gemm_kernel<T, EPI, PRE>.
+# bf16, the 6-launch blocks of --norms window and fold2).  The GEMM instances
+# are told apart by their (mangled) template arguments: gemm_kernel<T, EPI, PRE>.
 TRACE_NAMES = [
     ("_ZN3nsw11gemm_kernelIDF16bLi2ELi3E", "fc1_rowscale"),
+    ("_ZN3nsw11gemm_kernelIDF16bLi64ELi3E", "qkv_rowscale"),
+    ("_ZN3nsw11gemm_kernelIDF16bLi13ELi0E", "proj_sumsq"),
+    ("_ZN3nsw11gemm_kernelIDF16bLi14ELi0E", "fc2_to_tokens"),
+    ("partition_sumsq_kernel", "partition_sumsq"),
     ("_ZN3nsw11gemm_kernelIDF16bLi3ELi0E", "fc2"),
     ("_ZN3nsw11gemm_kernelIDF16bLi64ELi0E", "qkv"),
     ("_ZN3nsw11gemm_kernelIDF16bLi11ELi0E", "proj_scatter_sumsq"),

@@ -187,10 +187,14 @@ typedef struct nsw_block_params {
   const void* b2;        /* [C]          mlp.bias2.bias                         */
   /* Optional norm-folded weights: w1_n2[n,k] = w1[n,k] * norm2_w[k] removes
    * the norm2 pass (the proj GEMM writes h1's row sums of squares, fc1 applies
-   * the row scale: 6 launches, the faster form); wqkv_n1[n,k] = wqkv[n,k] *
-   * norm1_w[k] also folds norm1 into the QKV GEMM (5 launches; that GEMM
-   * then gathers token rows and sums their squares itself, which measured
-   * slower on MI355X than the separate norm1 gather). */
+   * the row scale); wqkv_n1[n,k] = wqkv[n,k] * norm1_w[k] folds norm1 into
+   * the QKV GEMM.  Both given: the block runs as the one-block window-order
+   * chain of nsw_swin_blocks_forward (partition + norm1 sums, QKV with norm1
+   * as a row scale, attention, proj + norm2 sums in window order, fc1, fc2
+   * scattering to tokens: 6 launches, the fastest form).  w1_n2 alone: norm1
+   * gather, proj scattering to tokens with the sums (6 launches).  wqkv_n1
+   * alone: the QKV GEMM gathers token rows and sums their squares itself
+   * (slower), norm2 as a pass. */
   const void* wqkv_n1;   /* [3C, C] or NULL                                     */
   const void* w1_n2;     /* [Hm, C] or NULL                                     */
 } nsw_block_params;
@@ -207,7 +211,8 @@ typedef struct nsw_block_shape {
                            /* 1: tanh form (the TE block's "gelu")              */
 } nsw_block_shape;
 
-/* Bytes of device workspace nsw_swin_block_forward needs. */
+/* Bytes of device workspace nsw_swin_block_forward needs (for any choice
+ * of the optional weights). */
 size_t nsw_block_workspace_size(const nsw_block_shape* s);
 
 /* y = Block.forward(x); x and y [B,T,H,W,C] must not alias. */
@@ -316,6 +321,35 @@ int nsw_linear_rownorm(const void* x, const void* w_n, const void* bias, const v
 int nsw_linear_rowscale(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
                         const float* row_sumsq, int64_t nparts, int64_t M, int64_t N, int64_t K,
                         int epilogue, float eps, int dtype, void* stream);
+
+/* WindowMultiHeadAttention's q/k/v projections with their per-head q/k
+ * RMSNorms (models/swin_helpers.py:212-241) on rows whose norm1
+ * (swin_helpers.py:446, nn.RMSNorm) comes as a row scale from partial sums of
+ * squares supplied by the rows' producer: qkv[m] = headnorm(rs[m] *
+ * (x[m] . wqkv_n^T) + bqkv), wqkv_n = wqkv * norm1_w per input column, rs[m]
+ * = 1/sqrt(sum_p row_sumsq[m*nparts + p] / C + eps).  x [M, C] in any row
+ * order (window order in the blocks), qkv [M, 3C]; row_sumsq 16-byte
+ * aligned.  Requires C % 64 == 0, hd in {16,32,64}. */
+int nsw_qkv_projection_rowscale(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w,
+                                const void* kn_w, float eps, void* qkv, const float* row_sumsq,
+                                int64_t nparts, int64_t M, int64_t C, int64_t num_heads, int dtype,
+                                void* stream);
+
+/* The residual adds of Block.forward (models/swin_helpers.py:452-458: x +
+ * attn-branch, h1 + mlp-branch) on window-ordered rows: y[map(m)] = x[m] .
+ * w^T + bias + residual[m], and, for map modes 0 and 2, the stored rows'
+ * partial sums of squares into row_sumsq [rows, nparts] at the same rows
+ * (nparts = nsw_row_sumsq_parts(N, dtype): the statistics of the norm that
+ * consumes y).  map_mode 0: map(m) = m; 1: the token of window row m of the
+ * image (B,T,H,W, window ws, shift s) — window_reverse + roll by +shift,
+ * :424-431; 2: that token's row in the window order of the same image with
+ * shift (sa, sb) — the next block's roll + window_partition, :402-412.
+ * row_sumsq NULL for mode 1, required otherwise.  Requirements as
+ * nsw_linear; residual and y must not alias. */
+int nsw_linear_remap_residual(const void* x, const void* w, const void* bias, const void* residual, void* y,
+                              float* row_sumsq, int64_t M, int64_t N, int64_t K, int map_mode, int64_t B,
+                              int64_t T, int64_t H, int64_t W, int64_t ws0, int64_t ws1, int64_t s0,
+                              int64_t s1, int64_t sa, int64_t sb, int dtype, void* stream);
 
 /* Patch matrix of the stride-p patch convolution (PatchEmbedLayer,
  * models/layer_helpers.py:120-172, as called by SwinTransformer.prepare_tokens,

@@ -73,9 +73,16 @@ static BlockLayout block_layout(const nsw_block_shape* s) {
 
 using namespace nsw;
 
+namespace nsw {
+static size_t chain_workspace(const nsw_block_shape* s);
+}
+
 extern "C" size_t nsw_block_workspace_size(const nsw_block_shape* s) {
   if (!s || s->B <= 0 || s->T <= 0 || s->H <= 0 || s->W <= 0 || s->C <= 0 || s->hidden <= 0) return 0;
-  return block_layout(s).total;
+  // the larger of the two forms (the one-block window-order chain runs when
+  // both norm-folded weights are given)
+  const size_t a = block_layout(s).total, b = chain_workspace(s);
+  return a > b ? a : b;
 }
 
 extern "C" int nsw_swin_block_forward(const void* x, void* y, const nsw_block_params* p,
@@ -102,6 +109,11 @@ extern "C" int nsw_swin_block_forward(const void* x, void* y, const nsw_block_pa
   NSW_CHECK_ARG(s->gelu_tanh == 0 || s->gelu_tanh == 1, "%s: gelu_tanh must be 0 or 1", what);
   const int gelu_epi = s->gelu_tanh ? NSW_EPI_BIAS_GELU_TANH : NSW_EPI_BIAS_GELU;
   int rc;
+  if (p->wqkv_n1 && p->w1_n2) {
+    // both norms folded: the one-block window-order chain (h1 stays in
+    // window order, fc2 scatters to tokens)
+    return nsw_swin_blocks_forward(x, y, p, s, 1, workspace, workspace_bytes, stream);
+  }
   if (p->wqkv_n1) {
     // K2'
     rc = gemm_qkv_norm_gather(x, p->wqkv_n1, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, s->B, s->T, s->H, s->W, C,
@@ -186,6 +198,8 @@ static ChainLayout chain_layout(const nsw_block_shape* s) {
   l.total = l.s2 + ss;
   return l;
 }
+
+static size_t chain_workspace(const nsw_block_shape* s) { return chain_layout(s).total; }
 
 static bool same_stack(const nsw_block_shape* a, const nsw_block_shape* b) {
   return a->B == b->B && a->T == b->T && a->H == b->H && a->W == b->W && a->C == b->C &&

@@ -873,3 +873,20 @@ extern "C" int nsw_linear_rowscale(const void* x, const void* w_n, const void* b
                                    int64_t K, int epilogue, float eps, int dtype, void* stream) {
   return gemm_linear_rowscale(x, w_n, bias, residual, y, row_sumsq, nparts, M, N, K, epilogue, eps, dtype, stream);
 }
+
+extern "C" int nsw_qkv_projection_rowscale(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w,
+                                           const void* kn_w, float eps, void* qkv, const float* row_sumsq,
+                                           int64_t nparts, int64_t M, int64_t C, int64_t num_heads, int dtype,
+                                           void* stream) {
+  return gemm_qkv_rowscale(x, wqkv_n, bqkv, qn_w, kn_w, eps, qkv, row_sumsq, nparts, M, C, num_heads, dtype,
+                           stream);
+}
+
+extern "C" int nsw_linear_remap_residual(const void* x, const void* w, const void* bias, const void* residual,
+                                         void* y, float* row_sumsq, int64_t M, int64_t N, int64_t K, int map_mode,
+                                         int64_t B, int64_t T, int64_t H, int64_t W, int64_t ws0, int64_t ws1,
+                                         int64_t s0, int64_t s1, int64_t sa, int64_t sb, int dtype,
+                                         void* stream) {
+  return gemm_linear_remap(x, w, bias, residual, y, row_sumsq, M, N, K, map_mode, B, T, H, W, ws0, ws1, s0, s1,
+                           sa, sb, dtype, stream);
+}

@@ -90,6 +90,10 @@ SIGNATURES = {
     "nsw_linear_rowscale": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _f32, _int,
                                    _vp]),
     "nsw_row_sumsq_parts": (_i64, [_i64, _int]),
+    "nsw_qkv_projection_rowscale": (_int, [_vp, _vp, _vp, _vp, _vp, _f32, _vp, _vp, _i64, _i64, _i64, _i64, _int,
+                                           _vp]),
+    "nsw_linear_remap_residual": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _i64, _i64, _i64,
+                                         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp]),
     "nsw_proj_reverse_residual_sumsq": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                                _i64, _i64, _i64, _i64, _int, _vp]),
     "nsw_patch_im2col": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _int,

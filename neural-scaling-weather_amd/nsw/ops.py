@@ -365,6 +365,53 @@ def linear_rowscale(x: torch.Tensor, w_n: torch.Tensor, row_sumsq: torch.Tensor,
     return y
 
 
+def qkv_projection_rowscale(x: torch.Tensor, wqkv_n: torch.Tensor, bqkv: torch.Tensor, qn_w: torch.Tensor,
+                            kn_w: torch.Tensor, row_sumsq: torch.Tensor, num_heads: int,
+                            eps: Optional[float] = None) -> torch.Tensor:
+    """[M, C] -> [M, 3C]: q|k|v of RMSNorm(x) (norm1's weight folded into
+    wqkv_n) with the row statistics given as partial sums of squares
+    row_sumsq [M, P] (from window_partition_sumsq or linear_remap_residual)."""
+    dev = _dev(x, wqkv_n, bqkv, qn_w, kn_w, row_sumsq)
+    _same_dtype(x, wqkv_n, bqkv, qn_w, kn_w)
+    C = x.shape[-1]
+    M = x.numel() // C
+    if row_sumsq.dtype != torch.float32 or row_sumsq.dim() != 2 or row_sumsq.shape[0] != M:
+        raise ValueError("qkv_projection_rowscale: row_sumsq must be a contiguous fp32 [M, P] tensor")
+    eps = default_eps(x.dtype) if eps is None else float(eps)
+    y = torch.empty(x.shape[:-1] + (3 * C,), dtype=x.dtype, device=dev)
+    check(lib().nsw_qkv_projection_rowscale(x.data_ptr(), wqkv_n.data_ptr(), bqkv.data_ptr(), qn_w.data_ptr(),
+                                            kn_w.data_ptr(), eps, y.data_ptr(), row_sumsq.data_ptr(),
+                                            row_sumsq.shape[1], M, C, num_heads, dtype_code(x), _stream(dev)),
+          "qkv_projection_rowscale")
+    return y
+
+
+def linear_remap_residual(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, residual: torch.Tensor,
+                          map_mode: int, image=None, window_size=(1, 1), shift_size=(0, 0), next_shift=(0, 0)):
+    """(y, row_sumsq): y[map(m)] = x[m] . w^T + bias + residual[m] for window
+    rows of ``image`` = (B, T, H, W) with ``window_size`` / ``shift_size``:
+    map_mode 0 identity, 1 to token order, 2 to the window order of the
+    same image rolled by ``next_shift``; row_sumsq [M, P] fp32 (the stored
+    rows' partial sums of squares, at the stored rows) for modes 0 and 2,
+    None for mode 1."""
+    dev = _dev(x, w, bias, residual)
+    _same_dtype(x, w, bias, residual)
+    K = x.shape[-1]
+    N = w.shape[0]
+    M = x.numel() // K
+    B, T, H, W = image if image is not None else (1, 1, 1, M)
+    y = torch.empty(M, N, dtype=x.dtype, device=dev)
+    ss = None
+    if map_mode != 1:
+        ss = torch.empty(M, lib().nsw_row_sumsq_parts(N, dtype_code(x)), dtype=torch.float32, device=dev)
+    check(lib().nsw_linear_remap_residual(x.data_ptr(), w.data_ptr(), bias.data_ptr(), residual.data_ptr(),
+                                          y.data_ptr(), _p(ss), M, N, K, int(map_mode), B, T, H, W,
+                                          window_size[0], window_size[1], int(shift_size[0]), int(shift_size[1]),
+                                          int(next_shift[0]), int(next_shift[1]), dtype_code(x), _stream(dev)),
+          "linear_remap_residual")
+    return y, ss
+
+
 # ------------------------------------------------------------------- block ---
 
 _ws_lock = threading.Lock()

@@ -184,13 +184,15 @@ class Block(nn.Module):
             H, W, self.window_size, self.shift_size, temporal_context_window_size), persistent=False)
         self._pack_key = None
         self._pack = None
-        # fold_norm2: the proj GEMM writes the row sums of squares of h1 and
-        # fc1 applies RMSNorm as a row scale with norm2's weight folded into
-        # W1 (no separate norm2 pass; 6 launches).  fold_norm1: also fold
-        # norm1 into the QKV GEMM, which then gathers the token rows and sums
-        # their squares in its main loop (5 launches) -- slower on MI355X than
-        # the separate norm1 gather (2.14 vs 2.01 ms at 180x360, C=1024), so
-        # off by default.
+        # fold_norm2 (default): fc1 applies norm2 as a row scale (norm2's
+        # weight folded into W1) from row sums of squares written by the
+        # proj GEMM (no norm2 pass; 6 launches).  fold_norm1 as well: the
+        # block runs as a one-block window-order chain -- a partition pass
+        # that also writes the norm1 row sums, the QKV GEMM with norm1 as a
+        # row scale, h1 kept in window order, fc2 scattering to tokens (6
+        # launches, the same time at config 2).  fold_norm1 alone: the QKV
+        # GEMM gathers the token rows and sums their squares in its main
+        # loop (slower).
         self.fold_norm1 = False
         self.fold_norm2 = True
 

@@ -171,3 +171,84 @@ def test_chain_argument_errors(device):
         ops.swin_blocks_forward(x, bad, 2, (9, 18), [(0, 0), (4, 9)])
     with pytest.raises(ValueError, match="alias"):
         ops.swin_blocks_forward(x, packs, 2, (9, 18), [(0, 0), (4, 9)], out=x)
+
+
+def _partial_sumsq(rows: torch.Tensor, es: int) -> torch.Tensor:
+    """float32 [M, P] sums of squares per 512-byte part (float64 sums)."""
+    per = 512 // es
+    r = rows.double()
+    C = r.shape[1]
+    return torch.stack([(r[:, p * per:(p + 1) * per] ** 2).sum(1) for p in range(-(-C // per))], 1).float()
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
+def test_qkv_projection_rowscale(device, dtype, tol):
+    """nsw_qkv_projection_rowscale against the oracle: per-head q/k RMSNorm of
+    RMSNorm(x; norm1) . [Wq;Wk;Wv]^T + b (models/swin_helpers.py:446, 212-241),
+    the row statistics given as 512-byte partial sums of x's squares."""
+    from nsw import ops
+    C, heads, M = 256, 4, 1000
+    p = synth.block_params(C, heads, seed=61, random_bias=True, random_norm=True)
+    p = {k: v.to(dtype).float() for k, v in p.items()}
+    x = synth.activations((M, C), seed=62).to(dtype).float()
+    eps = torch.finfo(dtype).eps
+    wqkv = torch.cat([p["attn.q.weight"], p["attn.k.weight"], p["attn.v.weight"]], 0)
+    bqkv = torch.cat([p["attn.biasq.bias"], p["attn.biask.bias"], p["attn.biasv.bias"]], 0)
+    n1 = p["norm1.norm.weight"]
+    wqkv_n = (wqkv * n1[None, :]).to(dtype)
+    ss = _partial_sumsq(x.to(dtype), torch.finfo(dtype).bits // 8)
+    d = lambda t: t.to(device, dtype).contiguous()
+    with torch.inference_mode():
+        got = ops.qkv_projection_rowscale(d(x), d(wqkv_n), d(bqkv), d(p["attn.q_norm.norm.weight"]),
+                                          d(p["attn.k_norm.norm.weight"]), ss.to(device), heads, eps)
+    torch.cuda.synchronize()
+    xn = ref.rms_norm(x, n1, eps)
+    lin = xn @ wqkv.T + bqkv
+    q, k, v = lin.split(C, dim=1)
+    hd = C // heads
+    q = ref.rms_norm(q.reshape(M, heads, hd), p["attn.q_norm.norm.weight"], eps).reshape(M, C)
+    k = ref.rms_norm(k.reshape(M, heads, hd), p["attn.k_norm.norm.weight"], eps).reshape(M, C)
+    want = torch.cat([q, k, v], 1)
+    assert rel_l2(got, want) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_linear_remap_residual(device, dtype, mode):
+    """nsw_linear_remap_residual: rows of x . w^T + b + residual stored at
+    the identity (0), the token of each window row (1) or that token's row in
+    the window order of another shift (2), with the stored rows' partial sums
+    of squares for modes 0 and 2 (index maps from oracle/index_maps.py)."""
+    from nsw import ops
+    from oracle import index_maps
+    B, T, H, W, ws, sh, sh2, K, N = 2, 1, 18, 36, (9, 18), (4, 9), (0, 0), 128, 256
+    M = B * T * H * W
+    g = torch.Generator().manual_seed(71)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(dtype)
+    b = torch.randn(N, generator=g).to(dtype)
+    r = torch.randn(M, N, generator=g).to(dtype)
+    with torch.inference_mode():
+        y, ss = ops.linear_remap_residual(x.to(device), w.to(device), b.to(device), r.to(device), mode,
+                                          image=(B, T, H, W), window_size=ws, shift_size=sh, next_shift=sh2)
+    torch.cuda.synchronize()
+    rows = x.double() @ w.double().T + b.double() + r.double()
+    tok = torch.from_numpy(index_maps.gather_rows(B, T, H, W, ws[0], ws[1], sh[0], sh[1]))
+    if mode == 0:
+        dest = torch.arange(M)
+    else:
+        dest = tok
+        if mode == 2:
+            tok2 = torch.from_numpy(index_maps.gather_rows(B, T, H, W, ws[0], ws[1], sh2[0], sh2[1]))
+            row_of_tok = torch.empty(M, dtype=torch.int64)
+            row_of_tok[tok2] = torch.arange(M)
+            dest = row_of_tok[tok]
+    want = torch.empty(M, N, dtype=torch.float64)
+    want[dest] = rows
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert rel_l2(y, want) < tol
+    if mode == 1:
+        assert ss is None
+    else:
+        es = 4 if dtype == torch.float32 else 2
+        torch.testing.assert_close(ss.cpu(), _partial_sumsq(y.cpu(), es), rtol=1e-5, atol=1e-5)

@@ -188,8 +188,10 @@ def test_linear_rowscale_rejects_bad_partials(device):
                                         (torch.bfloat16, (1, 1, 180, 360, 1024, 16, (9, 18), (4, 9))),
                                         (torch.bfloat16, (2, 2, 18, 36, 128, 2, (9, 18), (4, 9)))])
 def test_block_norm_folds(device, dtype, case):
-    """Block.forward with norm2 folded (6 launches, the default), both norms
-    folded (5) and neither (7) matches the oracle."""
+    """Block.forward with norm2 folded (6 launches: norm1 gather, proj
+    scatter; the default), both norms folded (the one-block window-order
+    chain, 6), norm1 folded into the gathering QKV GEMM (norm2 as a pass) and
+    neither (7) matches the oracle."""
     import nsw
     B, T, H, W, C, heads, ws, shift = case
     p = synth.block_params(C, heads, seed=41, random_bias=True, random_norm=True)
@@ -203,7 +205,7 @@ def test_block_norm_folds(device, dtype, case):
     outs = {}
     with torch.inference_mode():
         xd = x.to(device=device, dtype=dtype)
-        for f1, f2 in [(False, True), (True, True), (False, False)]:
+        for f1, f2 in [(True, True), (False, True), (True, False), (False, False)]:
             blk.fold_norm1, blk.fold_norm2 = f1, f2
             outs[(f1, f2)] = blk(xd)
     # the residual increment y - x is checked too; its error floor is what

@@ -56,8 +56,11 @@ def test_workspace_sizes_are_host_only(L):
     parts = 1024 * 2 // 512                      # row sums of squares: one float per 512 B of h1 row
     assert L.nsw_row_sumsq_parts(1024, _lib.NSW_DTYPE_BF16) == parts
     assert L.nsw_row_sumsq_parts(1024, _lib.NSW_DTYPE_F32) == 8
-    assert n >= M * (1024 + 4096 + 1024) * 2 + M * parts * 4
-    assert n < M * (1024 + 4096 + 1024) * 2 + M * parts * 4 + 4096
+    # the larger of the two block forms: the one-block window-order chain
+    # (two row buffers, qkv / u, o, h1, two sums arrays) when both norms are folded
+    assert n == L.nsw_blocks_workspace_size(ctypes.byref(s), 1)
+    assert n >= M * (4 * 1024 + 4096) * 2 + 2 * M * parts * 4
+    assert n < M * (4 * 1024 + 4096) * 2 + 2 * M * parts * 4 + 8 * 256
     assert L.nsw_weighted_metrics_workspace_size(70, 720, 1440) > 0
     bad = _lib.BlockShape(0, 1, 180, 360, 1024, 16, 9, 18, 4, 9, 4096, 1e-7, 1)
     assert L.nsw_block_workspace_size(bad) == 0
