@@ -1,13 +1,15 @@
 // MFMA GEMM y[M,N] = epilogue(x[M,K] . w[N,K]^T) for gfx950, with the Swin
 // block's epilogues fused in.
 //
-// Workgroup tile 256 (m) x 256 (n), one workgroup of 4 wavefronts per CU in a
-// 2 x 2 grid, each owning a 128 x 128 sub-tile of 16x16 fp32 accumulator
-// blocks (256 accumulator registers per lane).  A stage holds 128 bytes of k
-// (64 bf16) of the 256 x-rows and the 256 w-rows and is consumed as two MFMA
-// steps of 32 bf16; x lives in a ring of 3 slots and w in a ring of 2 slots of
-// 32 KB (all 160 KB of LDS), filled at a steady 8 copies per wave and MFMA
-// step (schedule at mainloop_256).  Whole 128-byte lines per copy.
+// Workgroup tile 256 (m) x 256 (n), one workgroup of 8 wavefronts per CU
+// (two per SIMD, so that one wave's MFMAs cover the other's LDS reads and
+// waits) in a 2 (m) x 4 (n) grid, each owning a 128 x 64 sub-tile of 16x16
+// fp32 accumulator blocks (128 accumulator registers per lane).  A stage holds
+// 128 bytes of k (64 bf16) of the 256 x-rows and the 256 w-rows and is
+// consumed as two MFMA steps of 32 bf16; x lives in a ring of 3 slots and w in
+// a ring of 2 slots of 32 KB (all 160 KB of LDS), filled at a steady 4 copies
+// per wave and MFMA step (schedule at mainloop_256).  Whole 128-byte lines
+// per copy.
 //
 // Operand staging: global -> LDS copies use gfx950's buffer_load_dwordx4 ...
 // lds (direct to LDS, no VGPR staging): each instruction writes 1 KB = 8 stage
@@ -15,8 +17,10 @@
 // fragment read (16 rows, same chunk) is bank-conflict free whether
 // ds_read_b128 is served in 8-lane phases over 32 banks or 16-lane phases over
 // 64 banks: slot = chunk ^ g(row & 15), g(r) = ((r >> 1) & 7) ^ ((r & 1) << 2).
-// The MFMAs of step k run from registers while the fragment reads of step k+1
-// are interleaved between them (register double buffering).  Barriers are bare
+// The MFMAs of step k run from registers while the activation fragments of
+// step k+1 are read between them (register double buffering); the four weight
+// fragments of a step are read at its start (single-buffered: the register
+// file of two waves per SIMD has no room for a second set).  Barriers are bare
 // s_barrier: __syncthreads() would add a fence that waits for every
 // outstanding copy.
 //
@@ -46,8 +50,11 @@ constexpr int MB = WTM / 16;        // 16x16 result blocks per wave along m
 constexpr int STEPB = 64;           // k bytes per row consumed by one MFMA step
 
 constexpr int BN = 256;             // weight rows (n) per workgroup tile
-constexpr int WTN = 128;            // wave tile (n)
+constexpr int WTN = 64;             // wave tile (n)
 constexpr int NB = WTN / 16;        // 16x16 result blocks per wave along n
+constexpr int WGM = BM / WTM;       // wave grid along m (2)
+constexpr int WGN = BN / WTN;       // wave grid along n (4)
+constexpr int NW = WGM * WGN;       // wavefronts per workgroup: 8, two per SIMD
 constexpr int ROWB = 128;           // k bytes per row and LDS stage (two MFMA steps)
 // LDS of the operand ring: x in 3 slots and w in 2 slots of 256 rows x 128 B
 constexpr int RING = 5 * 256 * ROWB;
@@ -122,32 +129,34 @@ __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk)
 // Main loop of the 256 x 256 tile.  Stage st holds 128 bytes of k of the 256
 // x rows and the 256 w rows.  x lives in a ring of 3 slots and w in a ring of
 // 2 slots of 32 KB (160 KB in all), so that the copies of a stage are issued
-// at a steady 8 instructions per wave and MFMA step:
+// at a steady 4 instructions per wave and MFMA step:
 //   step 2s+1 (the second step of stage s, after the barrier that frees the
 //              slots of stage s): w of stage s+2 into w slot s%2;
 //   step 2s+2 (the first step of stage s+1): x of stage s+3 into x slot s%3,
 // and the x copies (the operand with fewer sharers in L2) get 2-3 steps of
 // lead, the w copies 1-2.  At the start of step 2s+1 a wave waits for the
 // copies of stage s+1 (only x of stage s+2 may still be in flight), then
-// barrier.  Fragments of step k+1 are read during step k (register double
-// buffering), so a slot is free once the barrier at the start of the last
-// step of its stage has passed.
+// barrier.  The x fragments of step k+1 are read during step k (register
+// double buffering) and the w fragments of a step at its start, before that
+// barrier, so a slot is free once the barrier at the start of the last step
+// of its stage has passed.
 template <typename T, int PRE>
 __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X, const T* __restrict__ Wt, int M,
                                              int N, int K, int m0, int n0, const EpiArgs& ea,
-                                             f32x4 (&acc)[8][8], float (&ssr)[8], int wave, int lane) {
+                                             f32x4 (&acc)[NB][MB], float (&ssr)[MB], int wave, int lane) {
   constexpr int SLOT = 256 * ROWB;        // one operand's stage: 32 KB
-  constexpr int NC = SLOT / (4 * 1024);   // copies per wave per operand and stage (8)
+  constexpr int NC = SLOT / (NW * 1024);  // copies per wave per operand and stage (4)
+  constexpr int WR = 256 / NW;            // stage rows copied by one wave (32)
   constexpr int UNR = 12;                 // steps per loop iteration: 6 stages, a multiple of 3 and 2
   const uint32_t rowbytes = (uint32_t)K * sizeof(T);
   const u32x4 rx = make_rsrc(X, (uint32_t)M * rowbytes);
   const u32x4 rw = make_rsrc(Wt, (uint32_t)N * rowbytes);
-  // copy j of this wave covers slot rows wave*64 + 8j .. +7; lane i writes row
+  // copy j of this wave covers slot rows wave*WR + 8j .. +7; lane i writes row
   // +i/8, 16-byte slot i%8, and loads global chunk slot ^ swizzle(row)
   uint32_t vx[NC], vw[NC];
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
-    const int srow = wave * 64 + j * 8 + lane / 8;
+    const int srow = wave * WR + j * 8 + lane / 8;
     const int chunk = (lane % 8) ^ row_swizzle(srow);
     int gx = m0 + srow;
     gx = gx < M ? gx : M - 1;   // rows past the edge re-read the last row (never stored)
@@ -157,7 +166,7 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
     vx[j] = (uint32_t)gx * rowbytes + chunk * 16;
     vw[j] = (uint32_t)gw * rowbytes + chunk * 16;
   }
-  const uint32_t cbase = (uint32_t)(uintptr_t)smem + wave * 64 * ROWB;   // this wave's first slot row
+  const uint32_t cbase = (uint32_t)(uintptr_t)smem + wave * WR * ROWB;   // this wave's first slot row
 
 #define NSW_XSLOT(s) (((s) % 3) * SLOT)
 #define NSW_WSLOT(s) ((3 + (s) % 2) * SLOT)
@@ -185,13 +194,11 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
   wg_barrier();
 
   const int frow = lane & 15, fg = lane >> 4;
-  const int wrow = (wave & 1) * 128 + frow;    // w rows of this wave (A operand)
-  const int xrow = (wave >> 1) * 128 + frow;   // x rows of this wave (B operand)
-  u32x4 fa[2][8], fb[2][8];
+  const int wrow = (wave % WGN) * WTN + frow;  // w rows of this wave (A operand)
+  const int xrow = (wave / WGN) * WTM + frow;  // x rows of this wave (B operand)
+  u32x4 fa[NB], fb[2][MB];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) fa[0][i] = lds_frag(smem + NSW_WSLOT(0), wrow + i * 16, fg);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) fb[0][i] = lds_frag(smem + NSW_XSLOT(0), xrow + i * 16, fg);
+  for (int i = 0; i < MB; ++i) fb[0][i] = lds_frag(smem + NSW_XSLOT(0), xrow + i * 16, fg);
 
   // step k = kt + U of stage st = k/2; kt is a multiple of UNR, so the slots
   // of the stages touched by step U are compile-time constants.  Step k
@@ -210,6 +217,10 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
       constexpr int sub_ = (U) % 2, su_ = (U) / 2;                                             \
       constexpr int nsub_ = ((U) + 1) % 2, nsu_ = ((U) + 1) / 2;                               \
       const int st = k >> 1;                                                                   \
+      /* this step's weight fragments, read before the barrier below: after */                 \
+      /* it the second step of a stage overwrites the stage's w slot         */                 \
+      _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                        \
+        fa[nb] = lds_frag(smem + NSW_WSLOT(su_), wrow + nb * 16, sub_ * 4 + fg);                \
       if (sub_ == 1 && k + 1 < nk) {                                                           \
         NSW_WAIT_VMCNT(NC);                                                                    \
         NSW_WAIT_LGKMCNT0();                                                                   \
@@ -217,18 +228,19 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
       }                                                                                        \
       const uint32_t wdst_ = cbase + (k + 1 < nk ? NSW_WSLOT(su_ + 2) : NSW_XSLOT(su_ + 1));    \
       const int cst_ = st + 2 < nst ? st + 2 : nst - 1;   /* past the end: the last stage, in L2 */ \
-      _Pragma("unroll") for (int mb = 0; mb < 8; ++mb) {                                       \
-        if (sub_ == 1) dma16(rw, wdst_ + mb * 1024, vw[mb], cst_ * ROWB);                      \
-        else NSW_COPY_X(su_ + 2, cst_, mb);                                                    \
+      _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                      \
+        if (mb < NC) {                                                                         \
+          if (sub_ == 1) dma16(rw, wdst_ + mb * 1024, vw[mb], cst_ * ROWB);                    \
+          else NSW_COPY_X(su_ + 2, cst_, mb);                                                  \
+        }                                                                                      \
         /* unconditional: after the last step these read stale slots (unused); a  */         \
         /* conditional read would make the wait-count pass drain all LDS reads   */         \
         fb[((U) + 1) & 1][mb] = lds_frag(smem + NSW_XSLOT(nsu_), xrow + mb * 16, nsub_ * 4 + fg); \
-        fa[((U) + 1) & 1][mb] = lds_frag(smem + NSW_WSLOT(nsu_), wrow + mb * 16, nsub_ * 4 + fg); \
-        _Pragma("unroll") for (int nb = 0; nb < 8; ++nb)                                       \
-          mfma_chunk<T>(acc[nb][mb], fa[(U) & 1][nb], fb[(U) & 1][mb]);                        \
+        _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                      \
+          mfma_chunk<T>(acc[nb][mb], fa[nb], fb[(U) & 1][mb]);                                 \
         if constexpr (pre_sums_in_loop(PRE)) ssr[mb] = frag_sumsq<T>(fb[(U) & 1][mb], ssr[mb]); \
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                                     \
-        __builtin_amdgcn_sched_group_barrier(0x008, 8 * (sizeof(T) == 2 ? 1 : 4), 0);          \
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
+        __builtin_amdgcn_sched_group_barrier(0x008, NB * (sizeof(T) == 2 ? 1 : 4), 0);         \
       }                                                                                        \
     }                                                                                          \
   }
@@ -246,7 +258,7 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
 }
 
 template <typename T, int EPI, int PRE>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, const T* __restrict__ Wt,
+__global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ X, const T* __restrict__ Wt,
                                                      T* __restrict__ Y, int M, int N, int K, EpiArgs ea) {
   // the operand ring during the k loop, the output staging area in the
   // epilogue
@@ -255,7 +267,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
 
   const int MT = (M + BM - 1) / BM, NT = (N + BN - 1) / BN;
   // Tiles of one XCD run in groups of GROUP_M row blocks x all column blocks,
@@ -326,7 +338,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
   float p_bias = 0.f, p_nw = 0.f, p_rs = 1.f;
   if constexpr (EPI != EPI_NONE && PLDS) {
     const int n = n0 + tid;
-    p_bias = n < N ? to_f32(((const T*)ea.bias)[n]) : 0.f;
+    p_bias = tid < BN && n < N ? to_f32(((const T*)ea.bias)[n]) : 0.f;
   }
   if constexpr (HDQ > 0) {
     if (tid < 2 * HDQ) p_nw = to_f32(((const T*)(tid < HDQ ? ea.qn_w : ea.kn_w))[tid % HDQ]);
@@ -334,7 +346,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
   if constexpr (PRE == PRE_ROWSCALE) {
     // row m0 + tid's norm from the producer's partial sums of squares, added
     // in a fixed order (rows past M read row 0 and are never stored)
-    const int m = m0 + tid;
+    const int m = m0 + (tid < BM ? tid : 0);
     const float* pp = ea.row_sumsq + (int64_t)(m < M ? m : 0) * ea.nparts;
     float ss = 0.f;
     int q = 0;
@@ -413,7 +425,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
   constexpr int VEC = 16 / sizeof(T);                 // elements per 16-byte chunk
   constexpr int LPR = BN / VEC;                       // lanes per output row (32 bf16 / 64 f32)
   constexpr int RPI = 64 / LPR;                       // rows per copy instruction (2 / 1)
-  constexpr int ITER = S::ROWS / 4 / RPI;             // copy instructions per wave per pass
+  constexpr int ITER = S::ROWS / NW / RPI;            // copy instructions per wave per pass
   constexpr int BATCH = ITER < 8 ? ITER : 8;
   constexpr int NBAT = ITER / BATCH;
   static_assert(ITER % BATCH == 0, "batch");
@@ -430,11 +442,15 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
     // epilogue parameters, one element per thread: the tile's 256 bias
     // values, the q and k norm weights, the 256 row scales
     float* prm = reinterpret_cast<float*>(smem + PARAM_LDS);
-    if constexpr (EPI != EPI_NONE) prm[tid] = p_bias;
+    if constexpr (EPI != EPI_NONE) {
+      if (tid < BN) prm[tid] = p_bias;
+    }
     if constexpr (HDQ > 0) {
       if (tid < 2 * HDQ) prm[PRM_NW + tid] = p_nw;
     }
-    if constexpr (PRE == PRE_ROWSCALE) prm[PRM_RS + tid] = p_rs;
+    if constexpr (PRE == PRE_ROWSCALE) {
+      if (tid < BM) prm[PRM_RS + tid] = p_rs;
+    }
     NSW_WAIT_LGKMCNT0();
     wg_barrier();
 #pragma unroll
@@ -585,14 +601,15 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(const T* __restrict__ X, c
       }
     }
     if constexpr (SUMSQ) {
-      // one store of the pass's row sums per wave: lane l holds wave row
-      // l % WROWS, part n0 / 256 (bf16) or n0 / 128 + l / 32 (fp32)
+      // one store of the pass's row sums per wave: bf16, lane l < WROWS
+      // holds wave row l (part n0 / 256); fp32, lane l with l % 32 < WROWS
+      // holds wave row l % 32, part n0 / 128 + l / 32
       if (!SCAT || ea.row_sumsq != nullptr) {
-        const int rw = lane % WROWS;
+        const int rw = RPI == 2 ? lane : (lane & 31);
         const int m = m0 + prow0 + wave * WROWS + rw;
-        const int pcol = n0 + (RPI == 2 ? 0 : (lane / 32) * 32 * VEC);   // first column of the part
-        const int orw = MAPPED ? lmap : m;
-        if (m < M && pcol < N) ea.row_sumsq[(int64_t)orw * ea.nparts + pcol / (32 * VEC)] = ssacc;
+        const int pcol = n0 + (RPI == 2 ? 0 : (lane >> 5) * 32 * VEC);   // first column of the part
+        const int orw = MAPPED ? lmap : m;                                 // lmap: row lane % WROWS (= rw here)
+        if (rw < WROWS && m < M && pcol < N) ea.row_sumsq[(int64_t)orw * ea.nparts + pcol / (32 * VEC)] = ssacc;
       }
     }
     if (pass + 1 < S::PASSES) wg_barrier();          // before the next pass overwrites the staging rows
@@ -614,7 +631,7 @@ static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t
                 "%s: x, w, y and residual must be 16-byte aligned", what);
   NSW_CHECK_ARG(((M + BM - 1) / BM) * ((N + BN - 1) / BN) < (1LL << 31), "%s: too many tiles", what);
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_kernel<T, EPI, PRE>), dim3((unsigned)tiles), dim3(256), 0, st, (const T*)x, (const T*)w,
+  hipLaunchKernelGGL((gemm_kernel<T, EPI, PRE>), dim3((unsigned)tiles), dim3(NW * 64), 0, st, (const T*)x, (const T*)w,
                      (T*)y, (int)M, (int)N, (int)K, ea);
   return check_launch(what);
 }
