@@ -17,10 +17,12 @@
 // fragment read (16 rows, same chunk) is bank-conflict free whether
 // ds_read_b128 is served in 8-lane phases over 32 banks or 16-lane phases over
 // 64 banks: slot = chunk ^ g(row & 15), g(r) = ((r >> 1) & 7) ^ ((r & 1) << 2).
-// The MFMAs of step k run from registers while the activation fragments of
-// step k+1 are read between them (register double buffering); the four weight
-// fragments of a step are read at its start (single-buffered: the register
-// file of two waves per SIMD has no room for a second set).  Barriers are bare
+// The MFMAs of step k run from registers while the fragments of step k+1 are
+// read between them: the MFMAs go n block by n block, and the next step's
+// weight fragment of an n block is read into the registers that block's
+// MFMAs have just released, so the x fragments are double-buffered and the
+// w fragments take one set (the register file of two waves per SIMD has no
+// room for two of both).  Barriers are bare
 // s_barrier: __syncthreads() would add a fence that waits for every
 // outstanding copy.
 //
@@ -136,10 +138,9 @@ __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk)
 // and the x copies (the operand with fewer sharers in L2) get 2-3 steps of
 // lead, the w copies 1-2.  At the start of step 2s+1 a wave waits for the
 // copies of stage s+1 (only x of stage s+2 may still be in flight), then
-// barrier.  The x fragments of step k+1 are read during step k (register
-// double buffering) and the w fragments of a step at its start, before that
-// barrier, so a slot is free once the barrier at the start of the last step
-// of its stage has passed.
+// barrier.  The fragments of step k+1 are read during step k, so a slot is
+// free once the barrier at the start of the last step of its stage has
+// passed.
 template <typename T, int PRE>
 __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X, const T* __restrict__ Wt, int M,
                                              int N, int K, int m0, int n0, const EpiArgs& ea,
@@ -196,7 +197,9 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
   const int frow = lane & 15, fg = lane >> 4;
   const int wrow = (wave % WGN) * WTN + frow;  // w rows of this wave (A operand)
   const int xrow = (wave / WGN) * WTM + frow;  // x rows of this wave (B operand)
-  u32x4 fa[NB], fb[2][MB];
+  u32x4 fa[2][NB], fb[2][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) fa[0][i] = lds_frag(smem + NSW_WSLOT(0), wrow + i * 16, fg);
 #pragma unroll
   for (int i = 0; i < MB; ++i) fb[0][i] = lds_frag(smem + NSW_XSLOT(0), xrow + i * 16, fg);
 
@@ -217,10 +220,6 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
       constexpr int sub_ = (U) % 2, su_ = (U) / 2;                                             \
       constexpr int nsub_ = ((U) + 1) % 2, nsu_ = ((U) + 1) / 2;                               \
       const int st = k >> 1;                                                                   \
-      /* this step's weight fragments, read before the barrier below: after */                 \
-      /* it the second step of a stage overwrites the stage's w slot         */                 \
-      _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                        \
-        fa[nb] = lds_frag(smem + NSW_WSLOT(su_), wrow + nb * 16, sub_ * 4 + fg);                \
       if (sub_ == 1 && k + 1 < nk) {                                                           \
         NSW_WAIT_VMCNT(NC);                                                                    \
         NSW_WAIT_LGKMCNT0();                                                                   \
@@ -228,19 +227,33 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
       }                                                                                        \
       const uint32_t wdst_ = cbase + (k + 1 < nk ? NSW_WSLOT(su_ + 2) : NSW_XSLOT(su_ + 1));    \
       const int cst_ = st + 2 < nst ? st + 2 : nst - 1;   /* past the end: the last stage, in L2 */ \
-      _Pragma("unroll") for (int mb = 0; mb < MB; ++mb) {                                      \
-        if (mb < NC) {                                                                         \
-          if (sub_ == 1) dma16(rw, wdst_ + mb * 1024, vw[mb], cst_ * ROWB);                    \
-          else NSW_COPY_X(su_ + 2, cst_, mb);                                                  \
+      /* n-block-major: the first MFMAs of a step need only its first weight  */             \
+      /* fragment.  Per n block: one copy, MB/NB next-step x fragments, MB    */             \
+      /* MFMAs, then the next step's weight fragment nb into the registers    */             \
+      /* the MFMAs have just released (two sets of x fragments, one of w)      */             \
+      _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                      \
+        if (nb < NC) {                                                                         \
+          if (sub_ == 1) dma16(rw, wdst_ + nb * 1024, vw[nb], cst_ * ROWB);                    \
+          else NSW_COPY_X(su_ + 2, cst_, nb);                                                  \
         }                                                                                      \
         /* unconditional: after the last step these read stale slots (unused); a  */         \
         /* conditional read would make the wait-count pass drain all LDS reads   */         \
-        fb[((U) + 1) & 1][mb] = lds_frag(smem + NSW_XSLOT(nsu_), xrow + mb * 16, nsub_ * 4 + fg); \
-        _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                      \
-          mfma_chunk<T>(acc[nb][mb], fa[nb], fb[(U) & 1][mb]);                                 \
-        if constexpr (pre_sums_in_loop(PRE)) ssr[mb] = frag_sumsq<T>(fb[(U) & 1][mb], ssr[mb]); \
+        _Pragma("unroll") for (int q = 0; q < MB / NB; ++q) {                                  \
+          const int mq = nb * (MB / NB) + q;                                                   \
+          fb[((U) + 1) & 1][mq] = lds_frag(smem + NSW_XSLOT(nsu_), xrow + mq * 16, nsub_ * 4 + fg); \
+        }                                                                                      \
+        _Pragma("unroll") for (int mb = 0; mb < MB; ++mb)                                      \
+          mfma_chunk<T>(acc[nb][mb], fa[(U) & 1][nb], fb[(U) & 1][mb]);                        \
+        fa[((U) + 1) & 1][nb] = lds_frag(smem + NSW_WSLOT(nsu_), wrow + nb * 16, nsub_ * 4 + fg); \
+        if constexpr (pre_sums_in_loop(PRE)) {                                                 \
+          _Pragma("unroll") for (int q = 0; q < MB / NB; ++q) {                                \
+            const int mq = nb * (MB / NB) + q;                                                 \
+            ssr[mq] = frag_sumsq<T>(fb[(U) & 1][mq], ssr[mq]);                                 \
+          }                                                                                    \
+        }                                                                                      \
+        __builtin_amdgcn_sched_group_barrier(0x100, MB / NB, 0);                               \
+        __builtin_amdgcn_sched_group_barrier(0x008, MB * (sizeof(T) == 2 ? 1 : 4), 0);         \
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
-        __builtin_amdgcn_sched_group_barrier(0x008, NB * (sizeof(T) == 2 ? 1 : 4), 0);         \
       }                                                                                        \
     }                                                                                          \
   }
