@@ -373,6 +373,23 @@ int nsw_patch_im2col(const void* x, const void* inv, int64_t B, int64_t T, int64
 int nsw_unpatchify(const void* y, void* out, int64_t B, int64_t C_out, int64_t H, int64_t W,
                    int64_t p, int64_t out_bstride, int in_dtype, int out_dtype, void* stream);
 
+/* The head GEMM with the head layout fused into its write-out: replaces
+ * nsw_linear (no bias) followed by nsw_unpatchify in
+ * SwinTransformer.forward_head (models/swin.py:286-299, the Linear E ->
+ * C_out*p*p of :201-209, then the reshape + einsum).  x [B*(H/p)*(W/p), K]
+ * (dtype) holds the tokens (row (b, i, j)); w_perm [C_out*p*p, K] is the
+ * head weight with its rows permuted from the reference's (u*p + v)*C_out + c
+ * to c*p*p + u*p + v; pixel (c, i*p + u, j*p + v) of frame b goes to
+ * out[b*out_bstride + (c*H + i*p + u)*W + j*p + v] in out_dtype (dtype, or
+ * float32 for a bf16 GEMM: the bf16-rounded values widened, as nsw_linear +
+ * nsw_unpatchify give).  Requires p in {1, 2, 4, 8, 16}, p | H, p | W,
+ * K a multiple of 64 (bf16) / 32 (f32), out_bstride >= C_out*H*W and a
+ * multiple of p, out aligned to min(16, p * element size) bytes, x and
+ * w_perm 16-byte aligned. */
+int nsw_head_unpatchify(const void* x, const void* w_perm, void* out, int64_t B, int64_t C_out, int64_t H,
+                        int64_t W, int64_t p, int64_t K, int64_t out_bstride, int dtype, int out_dtype,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,8 @@
 // round-robin) works on a contiguous range of tiles, in groups of GROUP_M
 // row blocks x all column blocks (column-major inside a group), so that the
 // tiles in flight on an XCD share both row panels and weight panels in its L2.
+#include <algorithm>
+
 #include "nsw_gemm_common.h"
 
 namespace nsw {
@@ -149,6 +151,7 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
   constexpr int NC = SLOT / (NW * 1024);  // copies per wave per operand and stage (4)
   constexpr int WR = 256 / NW;            // stage rows copied by one wave (32)
   constexpr int UNR = 12;                 // steps per loop iteration: 6 stages, a multiple of 3 and 2
+  static_assert(MB == 8 && NB == 4, "the step's schedule assumes 8 x 4 result blocks per wave");
   const uint32_t rowbytes = (uint32_t)K * sizeof(T);
   const u32x4 rx = make_rsrc(X, (uint32_t)M * rowbytes);
   const u32x4 rw = make_rsrc(Wt, (uint32_t)N * rowbytes);
@@ -251,9 +254,14 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
             ssr[mq] = frag_sumsq<T>(fb[(U) & 1][mq], ssr[mq]);                                 \
           }                                                                                    \
         }                                                                                      \
-        __builtin_amdgcn_sched_group_barrier(0x100, MB / NB, 0);                               \
-        __builtin_amdgcn_sched_group_barrier(0x008, MB * (sizeof(T) == 2 ? 1 : 4), 0);         \
+        /* the group's three fragment reads spread over its MFMAs: 1, 2 MFMAs, 1, */            \
+        /* 3 MFMAs, 1, 3 MFMAs (bf16; four MFMA instructions per block in fp32)   */            \
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * (sizeof(T) == 2 ? 1 : 4), 0);          \
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
+        __builtin_amdgcn_sched_group_barrier(0x008, 3 * (sizeof(T) == 2 ? 1 : 4), 0);          \
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
+        __builtin_amdgcn_sched_group_barrier(0x008, 3 * (sizeof(T) == 2 ? 1 : 4), 0);          \
       }                                                                                        \
     }                                                                                          \
   }
@@ -268,6 +276,68 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
 #undef NSW_COPY_W
 #undef NSW_XSLOT
 #undef NSW_WSLOT
+}
+
+// P consecutive values between LDS / registers / global memory, as one
+// access where P * sizeof(V) is 2, 4, 8 or 16 bytes (16-byte pieces above).
+template <typename V, int P>
+__device__ __forceinline__ void copy_run(V* __restrict__ dst, const V* __restrict__ src) {
+  constexpr int B = P * (int)sizeof(V);
+  if constexpr (B >= 16) {
+#pragma unroll
+    for (int i = 0; i < B / 16; ++i) reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(src)[i];
+  } else if constexpr (B == 8) {
+    *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
+  } else if constexpr (B == 4) {
+    *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(src);
+  } else {
+    *reinterpret_cast<uint16_t*>(dst) = *reinterpret_cast<const uint16_t*>(src);
+  }
+}
+
+// EPI_UNPATCH write-out of the staged rows [r0, r0 + S::ROWS) of a tile: the
+// head layout of models/swin.py:286-299 (reshape [b, h, w, p, p, c], einsum
+// nthwpqc -> ntchpwq) with the head's output columns permuted to c p^2 +
+// dy p + dx (host side), so that a tile's 256 columns are the whole p x p
+// patches of 256 / p^2 channels.  A thread keeps one staged row (a token:
+// frame b, patch row py, patch column px) and walks the (channel, dy)
+// pairs; per pair one LDS read of the p values dx = 0 .. p-1 and one store
+// of p pixels into image row py p + dy.  Consecutive lanes hold consecutive
+// tokens, so a store instruction covers consecutive p-pixel runs of one
+// image row.  Values are rounded to T at staging, then widened to float for
+// a float image (as the separate GEMM + unpatchify would).
+template <typename T, int P>
+__device__ __forceinline__ void unpatch_copy_out(const char* stg, const EpiArgs& ea, int M, int N, int r0, int n0,
+                                                 int tid) {
+  using S = Stg<T>;
+  constexpr int CPT = BN / (P * P);                   // channels per tile
+  constexpr int TPR = NW * 64 / S::ROWS;              // threads per staged row (2 / 4)
+  const int tl = tid % S::ROWS;                       // staged row of this thread
+  const int m = r0 + tl;
+  if (m >= M) return;
+  const int wq = ea.img_W / P, hw = (ea.img_H / P) * wq;
+  const int b = m / hw, rr = m - b * hw, py = rr / wq, px = rr - py * wq;
+  const int64_t HW = (int64_t)ea.img_H * ea.img_W;
+  const int64_t pix0 = (int64_t)b * ea.img_bstride + (int64_t)(py * P) * ea.img_W + px * P;
+  const int c0 = n0 / (P * P);
+  const T* row = reinterpret_cast<const T*>(stg + tl * S::STRIDE);
+  for (int cd = tid / S::ROWS; cd < CPT * P; cd += TPR) {
+    const int cl = cd / P, dy = cd - cl * P;
+    const int c = c0 + cl;
+    if (c * P * P >= N) break;                        // columns past N: channels past C_out
+    const T* src = row + cl * P * P + dy * P;
+    const int64_t off = pix0 + c * HW + (int64_t)dy * ea.img_W;
+    if (ea.img_f32 && sizeof(T) == 2) {
+      T v[P];
+      copy_run<T, P>(v, src);
+      float f[P];
+#pragma unroll
+      for (int e = 0; e < P; ++e) f[e] = to_f32(v[e]);
+      copy_run<float, P>(reinterpret_cast<float*>(ea.img) + off, f);
+    } else {
+      copy_run<T, P>(reinterpret_cast<T*>(ea.img) + off, src);
+    }
+  }
 }
 
 template <typename T, int EPI, int PRE>
@@ -325,7 +395,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
     const int n = nw0 + nb * 16 + fg * 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) bv[nb][r] = 0.f;
-    if constexpr (EPI != EPI_NONE && !PLDS) load4<T>(bias + (n < N ? n : 0), bv[nb]);   // straight-line: one batch
+    if constexpr (EPI != EPI_NONE && EPI != EPI_UNPATCH && !PLDS)
+      load4<T>(bias + (n < N ? n : 0), bv[nb]);   // straight-line: one batch
   }
 
   // per-head RMSNorm (QKV epilogue): a head is HDQ/16 consecutive 16-column
@@ -549,6 +620,17 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
       }
     }
     wg_barrier();
+    if constexpr (EPI == EPI_UNPATCH) {
+      switch (ea.img_p) {
+        case 1: unpatch_copy_out<T, 1>(stg, ea, M, N, m0 + prow0, n0, tid); break;
+        case 2: unpatch_copy_out<T, 2>(stg, ea, M, N, m0 + prow0, n0, tid); break;
+        case 4: unpatch_copy_out<T, 4>(stg, ea, M, N, m0 + prow0, n0, tid); break;
+        case 8: unpatch_copy_out<T, 8>(stg, ea, M, N, m0 + prow0, n0, tid); break;
+        default: unpatch_copy_out<T, 16>(stg, ea, M, N, m0 + prow0, n0, tid); break;
+      }
+      if (pass + 1 < S::PASSES) wg_barrier();        // before the next pass overwrites the staging rows
+      continue;
+    }
 #pragma unroll
     for (int ib = 0; ib < NBAT; ++ib) {
       const int cur = ib & 1;
@@ -910,6 +992,42 @@ extern "C" int nsw_qkv_projection_rowscale(const void* x, const void* wqkv_n, co
                                            void* stream) {
   return gemm_qkv_rowscale(x, wqkv_n, bqkv, qn_w, kn_w, eps, qkv, row_sumsq, nparts, M, C, num_heads, dtype,
                            stream);
+}
+
+// The forecast head with its layout fused in: image = unpatchify(x . w_perm^T)
+// (models/swin.py:286-299), w_perm the head weight with its rows permuted
+// from the reference's (dy p + dx) C_out + c to c p^2 + dy p + dx.
+int gemm_head_unpatchify(const void* x, const void* w_perm, void* out, int64_t B, int64_t C_out, int64_t H,
+                         int64_t W, int64_t p, int64_t K, int64_t out_bstride, int dtype, int out_dtype,
+                         void* stream) {
+  const char* what = "nsw_head_unpatchify";
+  NSW_CHECK_ARG(B > 0 && C_out > 0 && H > 0 && W > 0 && K > 0, "%s: B, C_out, H, W, K must be positive", what);
+  NSW_CHECK_ARG(p == 1 || p == 2 || p == 4 || p == 8 || p == 16, "%s: p=%lld must be 1, 2, 4, 8 or 16", what,
+                (long long)p);
+  NSW_CHECK_ARG(H % p == 0 && W % p == 0, "%s: H=%lld, W=%lld not divisible by p=%lld", what, (long long)H,
+                (long long)W, (long long)p);
+  NSW_CHECK_ARG(dtype == NSW_DTYPE_BF16 || dtype == NSW_DTYPE_F32, "%s: unknown dtype %d", what, dtype);
+  NSW_CHECK_ARG(out_dtype == dtype || out_dtype == NSW_DTYPE_F32,
+                "%s: the image is in the GEMM's dtype or float32 (got %d for %d)", what, out_dtype, dtype);
+  NSW_CHECK_ARG(out_bstride >= C_out * H * W && out_bstride % p == 0,
+                "%s: out_bstride must cover one frame and be a multiple of p", what);
+  const int64_t oes = out_dtype == NSW_DTYPE_F32 ? 4 : 2;
+  NSW_CHECK_ARG(((uintptr_t)out % (uintptr_t)std::min<int64_t>(16, p * oes)) == 0,
+                "%s: out must be aligned to min(16, p * element size) bytes", what);
+  NSW_CHECK_ARG(B * out_bstride < (1LL << 40) && H * W < (1LL << 31), "%s: image too large", what);
+  EpiArgs ea{};
+  ea.img = out;
+  ea.img_bstride = out_bstride;
+  ea.img_C = (int)C_out; ea.img_H = (int)H; ea.img_W = (int)W; ea.img_p = (int)p;
+  ea.img_f32 = out_dtype == NSW_DTYPE_F32 && dtype == NSW_DTYPE_BF16;
+  const int64_t M = B * (H / p) * (W / p);
+  return dispatch_gemm<EPI_UNPATCH>(dtype, x, w_perm, nullptr, M, C_out * p * p, K, ea, stream, what);
+}
+
+extern "C" int nsw_head_unpatchify(const void* x, const void* w_perm, void* out, int64_t B, int64_t C_out,
+                                   int64_t H, int64_t W, int64_t p, int64_t K, int64_t out_bstride, int dtype,
+                                   int out_dtype, void* stream) {
+  return gemm_head_unpatchify(x, w_perm, out, B, C_out, H, W, p, K, out_bstride, dtype, out_dtype, stream);
 }
 
 extern "C" int nsw_linear_remap_residual(const void* x, const void* w, const void* bias, const void* residual,

@@ -17,6 +17,8 @@ enum Epi {
   EPI_REMAP_RESIDUAL = 12,   // bias, + residual[m], stored at row_of_row_shift(m), + row sums of squares
   EPI_RES_SUMSQ = 13,        // bias, + residual[m], stored at row m, + row sums of squares
   EPI_TOKEN_RESIDUAL = 14,   // bias, + residual[m], stored at token_of_row(m)
+  EPI_UNPATCH = 15,          // no bias; row m (a token) and column c p^2 + dy p + dx go to
+                             // pixel (dy, dx) of the token's patch in image plane c
   EPI_QKV_HN16 = 16,         // bias, then per-head RMSNorm of the q and k
   EPI_QKV_HN32 = 32,         // columns, for head dims 16 / 32 / 64
   EPI_QKV_HN64 = 64
@@ -57,6 +59,11 @@ struct EpiArgs {
   float* row_sumsq;
   int nparts;
   int dh, dw;   // EPI_REMAP_RESIDUAL: shift differences of geom.row_of_row_shift
+  // EPI_UNPATCH: image [B, 1, img_C, img_H, img_W], frames img_bstride
+  // elements apart, in float (img_f32) or the GEMM's dtype; patch img_p
+  void* img;
+  int64_t img_bstride;
+  int img_C, img_H, img_W, img_p, img_f32;
 };
 
 // GELU with the exact-erf form of nn.GELU(): 0.5 v (1 + erf(v / sqrt 2)).

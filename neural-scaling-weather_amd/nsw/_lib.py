@@ -99,6 +99,7 @@ SIGNATURES = {
     "nsw_patch_im2col": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _int,
                                 _int, _vp]),
     "nsw_unpatchify": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
+    "nsw_head_unpatchify": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
 }
 
 _lib = None

@@ -598,6 +598,46 @@ def unpatchify(y: torch.Tensor, B: int, C_out: int, H: int, W: int, p: int,
     return dst
 
 
+def head_weight_perm(weight: torch.Tensor, C_out: int, p: int) -> torch.Tensor:
+    """The head weight [p*p*C_out, E] (reference row (u*p + v)*C_out + c,
+    models/swin.py:201-209,293-299) with its rows reordered to c*p*p + u*p + v,
+    the order nsw_head_unpatchify takes."""
+    E = weight.shape[-1]
+    if weight.shape[0] != p * p * C_out:
+        raise ValueError(f"head weight has {weight.shape[0]} rows, expected p*p*C_out = {p * p * C_out}")
+    return weight.view(p * p, C_out, E).transpose(0, 1).reshape(C_out * p * p, E).contiguous()
+
+
+def head_unpatchify(x: torch.Tensor, w_perm: torch.Tensor, B: int, C_out: int, H: int, W: int, p: int,
+                    dtype: Optional[torch.dtype] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """unpatchify(x . W^T) in one launch: x [B*(H/p)*(W/p), E] tokens, w_perm
+    from head_weight_perm -> [B, 1, C_out, H, W] in ``dtype`` (x's dtype or
+    float32), or into ``out`` (frames contiguous, e.g. one slot of a ring
+    buffer) in out's dtype."""
+    if x.dim() != 2 or x.shape[0] != B * (H // p) * (W // p):
+        raise ValueError("head_unpatchify: x must be [B*(H/p)*(W/p), E]")
+    if w_perm.shape != (C_out * p * p, x.shape[1]):
+        raise ValueError(f"head_unpatchify: w_perm must be [{C_out * p * p}, {x.shape[1]}]")
+    if out is not None:
+        if tuple(out.shape) != (B, 1, C_out, H, W):
+            raise ValueError(f"head_unpatchify: out must be [{B}, 1, {C_out}, {H}, {W}]")
+        if out.stride()[2:] != (H * W, W, 1) or out.stride(0) < C_out * H * W:
+            raise ValueError("head_unpatchify: every frame of out must be contiguous")
+        bstride = out.stride(0)
+        dst = out
+    else:
+        dst = torch.empty(B, 1, C_out, H, W, dtype=dtype or x.dtype, device=x.device)
+        bstride = C_out * H * W
+    dev = _dev(x, w_perm)
+    if dst.device != dev:
+        raise RuntimeError("libnsw op arguments are on different devices")
+    _same_dtype(x, w_perm)
+    check(lib().nsw_head_unpatchify(x.data_ptr(), w_perm.data_ptr(), dst.data_ptr(), B, C_out, H, W, p,
+                                    x.shape[1], bstride, dtype_code(x), dtype_code(dst), _stream(dev)),
+          "head_unpatchify")
+    return dst
+
+
 def weighted_metrics_unnorm(pred: torch.Tensor, target: torch.Tensor, std: torch.Tensor, mean: torch.Tensor,
                             weights: torch.Tensor, clim: Optional[torch.Tensor] = None):
     """Weighted RMSE (and ACC with ``clim``) of pred * std + mean against

@@ -10,7 +10,8 @@ Forward path on the GPU (models/swin.py:301-323):
                   constant coordinate fields, computed once and cached until
                   its weights change.
   blocks          nsw.Block (the fused shifted-window block).
-  forward_head    GEMM E -> C_out*p*p (no bias) -> nsw_unpatchify.  forward()
+  forward_head    GEMM E -> C_out*p*p (no bias) with the head layout in its
+                  write-out (nsw_head_unpatchify).  forward()
                   applies the head to the last frame only, which equals the
                   reference's all-frame head followed by ``x[:, -1:]`` because
                   the head is per token.
@@ -233,6 +234,8 @@ class SwinTransformer(nn.Module):
         self.chain_blocks = True
         self._pos_key = None
         self._pos = None
+        self._head_key = None
+        self._head_w = None
 
     def _init_coords(self):
         """models/swin.py:227-244: coords [T, H, W, 4] = spatial (x, y, z) with
@@ -293,27 +296,46 @@ class SwinTransformer(nn.Module):
         return self.patch_embed.tokens(x, residual=pos, invariants=invariants, frame0=frame0)
 
     # ----------------------------------------------------------------- head --
+    def _head_weight(self) -> torch.Tensor:
+        """head.weight with its rows in the order of the fused head
+        (ops.head_weight_perm), cached until the weight changes; rebuilt each
+        call while torch.compile traces."""
+        W = self.head.weight
+        if torch.compiler.is_compiling():
+            return ops.head_weight_perm(W.detach(), self.out_chans, self.patch_size)
+        key = (W.data_ptr(), W._version, W.dtype, W.device)
+        if self._head_key != key:
+            with torch.no_grad():
+                self._head_w = ops.head_weight_perm(W.detach(), self.out_chans, self.patch_size)
+            self._head_key = key
+        return self._head_w
+
     def forward_head(self, x: torch.Tensor) -> torch.Tensor:
-        """models/swin.py:286-299: [B, T, h, w, E] -> [B, T, C_out, H, W]."""
+        """models/swin.py:286-299: [B, T, h, w, E] -> [B, T, C_out, H, W]: the
+        head GEMM with the reshape + einsum layout in its write-out."""
         b, t, h, w, c = x.shape
         p = self.patch_size
-        y = torch_ops.linear_epi(x.reshape(-1, c), self.head.weight)
-        out = torch.ops.nsw.unpatchify(y, b * t, self.out_chans, h * p, w * p, p, None)
+        out = torch.ops.nsw.head_unpatchify(x.reshape(-1, c), self._head_weight(), b * t, self.out_chans, h * p,
+                                            w * p, p, None)
         return out.view(b, t, self.out_chans, h * p, w * p)
 
     def _head_last(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Head of the last frame only: [B, T, h, w, E] -> [B, 1, C_out, H, W]
-        (into ``out`` when given, in out's dtype)."""
+        (into ``out`` when given, in out's dtype: the fused head writes bf16
+        or float32 images, other dtypes go through a bf16/f32 result)."""
         b, t, h, w, c = x.shape
         p = self.patch_size
-        W = self.head.weight
+        Wp = self._head_weight()
+        H, W = h * p, w * p
         if out is None:
-            y = torch_ops.linear_epi(x[:, t - 1].reshape(b * h * w, c), W)
-            return torch.ops.nsw.unpatchify(y, b, self.out_chans, h * p, w * p, p, None)
-        y = torch.empty(b * h * w, self.out_size, dtype=x.dtype, device=x.device)
+            return torch.ops.nsw.head_unpatchify(x[:, t - 1].reshape(b * h * w, c), Wp, b, self.out_chans, H, W, p,
+                                                 None)
+        if out.dtype not in (x.dtype, torch.float32):
+            out.copy_(self._head_last(x))
+            return out
         for bi in range(b):
-            ops.linear(x[bi, t - 1].view(h * w, c), W, out=y[bi * h * w:(bi + 1) * h * w])
-        return ops.unpatchify(y, b, self.out_chans, h * p, w * p, p, out=out)
+            ops.head_unpatchify(x[bi, t - 1].view(h * w, c), Wp, 1, self.out_chans, H, W, p, out=out[bi:bi + 1])
+        return out
 
     # -------------------------------------------------------------- forward --
     def forward(self, x: torch.Tensor, invariants: Optional[torch.Tensor] = None, frame0: int = 0,

@@ -235,6 +235,18 @@ def _(y, B, C_out, H, W, p, dtype):
     return y.new_empty((B, 1, C_out, H, W), dtype=dtype if dtype is not None else y.dtype)
 
 
+@torch.library.custom_op("nsw::head_unpatchify", mutates_args=())
+def head_unpatchify(x: torch.Tensor, w_perm: torch.Tensor, B: int, C_out: int, H: int, W: int, p: int,
+                    dtype: Optional[torch.dtype]) -> torch.Tensor:
+    """The head GEMM with the head layout in its write-out (w_perm from ops.head_weight_perm)."""
+    return ops.head_unpatchify(x.contiguous(), w_perm.contiguous(), B, C_out, H, W, p, dtype=dtype)
+
+
+@head_unpatchify.register_fake
+def _(x, w_perm, B, C_out, H, W, p, dtype):
+    return x.new_empty((B, 1, C_out, H, W), dtype=dtype if dtype is not None else x.dtype)
+
+
 # ---------------------------------------------------------------- metrics ---
 
 @torch.library.custom_op("nsw::weighted_metrics", mutates_args=())

@@ -80,6 +80,49 @@ def test_unpatchify_bit_exact(device, idt, odt, B, Co, H, W, p):
     assert torch.all(ring[:, 0] == 7) and torch.all(ring[:, 2] == 7)
 
 
+@pytest.mark.parametrize("dt,odt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                    (torch.float32, torch.float32)])
+@pytest.mark.parametrize("B,Co,H,W,p,E", [(1, 70, 32, 64, 4, 128), (2, 6, 12, 16, 2, 64),
+                                           (1, 70, 72, 144, 4, 64),    # 648 tokens, 5 column tiles
+                                           (2, 5, 36, 40, 4, 64),      # N = 80 < one tile
+                                           (1, 3, 16, 32, 8, 64), (1, 296, 4, 8, 1, 64), (1, 2, 32, 32, 16, 64)])
+def test_head_unpatchify_matches_two_launches(device, dt, odt, B, Co, H, W, p, E):
+    """nsw_head_unpatchify = nsw_linear (no bias) + nsw_unpatchify bit for bit
+    (both paths round the GEMM result to the GEMM dtype first)."""
+    import nsw
+    h, w = H // p, W // p
+    g = torch.Generator().manual_seed(Co * 31 + p)
+    x = torch.randn(B * h * w, E, generator=g).to(dt).to(device)
+    Wt = (torch.randn(p * p * Co, E, generator=g) * 0.1).to(dt).to(device)
+    y = nsw.ops.linear(x, Wt)
+    want = nsw.ops.unpatchify(y, B, Co, H, W, p, dtype=odt).cpu()
+    got = nsw.ops.head_unpatchify(x, nsw.ops.head_weight_perm(Wt, Co, p), B, Co, H, W, p, dtype=odt).cpu()
+    assert torch.equal(got, want)
+    # into one slot of a [B, T, C, H, W] ring buffer
+    ring = torch.full((B, 3, Co, H, W), 7.0, dtype=odt, device=device)
+    nsw.ops.head_unpatchify(x, nsw.ops.head_weight_perm(Wt, Co, p), B, Co, H, W, p, out=ring[:, 1:2])
+    ring = ring.cpu()
+    assert torch.equal(ring[:, 1:2], want)
+    assert torch.all(ring[:, 0] == 7) and torch.all(ring[:, 2] == 7)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_head_unpatchify_exact_against_bruteforce(device, dt):
+    """Small-integer operands make every product and sum exact in both dtypes,
+    so the fused head must equal the element-by-element head layout of the
+    exact product (oracle/model_ref.unpatchify_bruteforce)."""
+    import nsw
+    B, Co, H, W, p, E = 2, 6, 12, 20, 2, 64
+    h, w = H // p, W // p
+    g = torch.Generator().manual_seed(3)
+    x = torch.randint(-2, 3, (B * h * w, E), generator=g).float()
+    Wt = torch.randint(-2, 3, (p * p * Co, E), generator=g).float()
+    want = mr.unpatchify_bruteforce(x @ Wt.T, B, 1, h, w, p, Co)
+    got = nsw.ops.head_unpatchify(x.to(dt).to(device), nsw.ops.head_weight_perm(Wt.to(dt).to(device), Co, p),
+                                  B, Co, H, W, p, dtype=torch.float32).cpu()
+    assert torch.equal(got, want)
+
+
 def test_patch_embed_layer_is_conv2d(device):
     import nsw
     layer = nsw.PatchEmbedLayer(patch_size=4, in_chans=5, embed_dim=64, sp1_shapes=[16], sp2_shapes=[32])

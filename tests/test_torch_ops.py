@@ -15,7 +15,7 @@ from nsw import torch_ops
 
 OPS = ["swin_block", "swin_blocks", "linear", "rms_norm", "layer_norm", "qkv_projection", "window_attention",
        "window_partition", "window_reverse", "roll_hw", "roll_window_partition", "window_reverse_roll",
-       "patch_im2col", "unpatchify", "weighted_metrics"]
+       "patch_im2col", "unpatchify", "head_unpatchify", "weighted_metrics"]
 
 
 def meta(*shape, dtype=torch.bfloat16):
@@ -48,6 +48,8 @@ def test_shape_functions():
     pm = n.patch_im2col(meta(2, 3, 70, 72, 144, dtype=torch.float32), 4, 1152, torch.bfloat16, None, 0)
     assert pm.shape == (2 * 3 * 18 * 36, 1152) and pm.dtype == torch.bfloat16
     out = n.unpatchify(meta(2 * 18 * 36, 1120), 2, 70, 72, 144, 4, torch.float32)
+    assert out.shape == (2, 1, 70, 72, 144) and out.dtype == torch.float32
+    out = n.head_unpatchify(meta(2 * 18 * 36, 1024), meta(1120, 1024), 2, 70, 72, 144, 4, torch.float32)
     assert out.shape == (2, 1, 70, 72, 144) and out.dtype == torch.float32
     f = meta(2, 3, 70, 8, 16, dtype=torch.float32)
     r, a = n.weighted_metrics(f, f, meta(8, dtype=torch.float64), None)
@@ -107,12 +109,25 @@ def test_model_traces_into_one_graph():
     t = targets(cap.graphs[0])
     assert count(t, "swin_blocks") == 1          # the blocks as one window-order chain
     assert count(t, "patch_im2col") == 2         # the image and the coordinate embedding
-    assert count(t, "unpatchify") == 1
+    assert count(t, "head_unpatchify") == 1       # the head GEMM with the head layout fused
     model.chain_blocks = False
     cap = Capture()
     torch._dynamo.reset()
     torch.compile(model, backend=cap, fullgraph=True)(torch.randn(1, 1, C, H, W))
     assert count(targets(cap.graphs[0]), "swin_block") == 4
+
+
+def test_head_weight_perm_matches_the_head_layout():
+    """Row c*p*p + u*p + v of the permuted weight is the reference's head row
+    (u*p + v)*C_out + c (models/swin.py:201-209,293-299)."""
+    from nsw import ops
+    Co, p, E = 5, 3, 4
+    Wt = torch.randn(p * p * Co, E)
+    Wp = ops.head_weight_perm(Wt, Co, p)
+    for c in range(Co):
+        for u in range(p):
+            for v in range(p):
+                assert torch.equal(Wp[c * p * p + u * p + v], Wt[(u * p + v) * Co + c])
 
 
 def test_metric_traces_into_one_graph():
