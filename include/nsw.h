@@ -237,6 +237,17 @@ int nsw_swin_blocks_forward(const void* x, void* y, const nsw_block_params* para
                             const nsw_block_shape* shapes, int64_t depth, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/* nsw_swin_blocks_forward from block 0's input already in block 0's window
+ * order with its norm1 statistics: xw [B*T*H*W, C] as nsw_roll_window_partition
+ * (shift shapes[0].s0, s1) lays out the tokens, row_sumsq [B*T*H*W, nparts]
+ * fp32 (16-byte aligned) as nsw_window_partition_sumsq writes them -- e.g. the
+ * patch-embedding GEMM of models/swin.py:269-284 with nsw_linear_remap_residual
+ * map mode 3.  xw and row_sumsq are read only; y in token order.  5*depth
+ * launches. */
+int nsw_swin_blocks_forward_windowed(const void* xw, const float* row_sumsq, void* y,
+                                     const nsw_block_params* params, const nsw_block_shape* shapes,
+                                     int64_t depth, void* workspace, size_t workspace_bytes, void* stream);
+
 /* WeightedRMSE.forward (utils/losses.py:243-266) and the textbook weighted ACC.
  * pred/target fp32 [P, H, W] with P = B*T*Cch planes (channel = plane % Cch);
  * w float64 [H, w_cols] with w_cols = 1 (cos-lat weights, the inference path,
@@ -343,8 +354,10 @@ int nsw_qkv_projection_rowscale(const void* x, const void* wqkv_n, const void* b
  * consumes y).  map_mode 0: map(m) = m; 1: the token of window row m of the
  * image (B,T,H,W, window ws, shift s) — window_reverse + roll by +shift,
  * :424-431; 2: that token's row in the window order of the same image with
- * shift (sa, sb) — the next block's roll + window_partition, :402-412.
- * row_sumsq NULL for mode 1, required otherwise.  Requirements as
+ * shift (sa, sb) — the next block's roll + window_partition, :402-412; 3:
+ * row m is token m and map(m) its row in the window order of the image with
+ * shift s (roll + window_partition of token-ordered rows: the first block's
+ * input).  row_sumsq NULL for mode 1, required otherwise.  Requirements as
  * nsw_linear; residual and y must not alias. */
 int nsw_linear_remap_residual(const void* x, const void* w, const void* bias, const void* residual, void* y,
                               float* row_sumsq, int64_t M, int64_t N, int64_t K, int map_mode, int64_t B,

@@ -215,12 +215,17 @@ extern "C" size_t nsw_blocks_workspace_size(const nsw_block_shape* shapes, int64
   return chain_layout(s).total;
 }
 
-extern "C" int nsw_swin_blocks_forward(const void* x, void* y, const nsw_block_params* params,
-                                       const nsw_block_shape* shapes, int64_t depth, void* workspace,
-                                       size_t workspace_bytes, void* stream) {
-  const char* what = "nsw_swin_blocks_forward";
-  NSW_CHECK_ARG(x && y && params && shapes && depth > 0, "%s: null argument or depth <= 0", what);
-  NSW_CHECK_ARG(x != (const void*)y, "%s: x and y must not alias", what);
+// The chain from token-ordered x (partitioned here into block 0's window
+// order with its norm1 row sums), or from x0w / s0w already in that form
+// (read only: block 0 takes its rows and sums from there, later blocks from
+// the workspace).
+static int blocks_chain(const void* x, const void* x0w, const float* s0w, void* y, const nsw_block_params* params,
+                        const nsw_block_shape* shapes, int64_t depth, void* workspace, size_t workspace_bytes,
+                        void* stream, const char* what) {
+  const void* in = x ? x : x0w;
+  NSW_CHECK_ARG(in && y && params && shapes && depth > 0, "%s: null argument or depth <= 0", what);
+  NSW_CHECK_ARG(in != (const void*)y, "%s: x and y must not alias", what);
+  NSW_CHECK_ARG(x != nullptr || s0w != nullptr, "%s: the window-ordered input needs its row sums", what);
   const nsw_block_shape* s0 = shapes;
   NSW_CHECK_ARG(s0->num_heads > 0 && s0->C % s0->num_heads == 0 && s0->hidden > 0,
                 "%s: C not divisible by num_heads, or hidden <= 0", what);
@@ -247,16 +252,20 @@ extern "C" int nsw_swin_blocks_forward(const void* x, void* y, const nsw_block_p
   const int64_t hd = C / s0->num_heads;
   const int dt = s0->dtype;
   const int64_t nparts = sumsq_parts(C, dt);
-  int rc = nsw_window_partition_sumsq(x, X[0], S1, B, T, H, W, C, s0->ws0, s0->ws1, shapes[0].s0, shapes[0].s1,
-                                      dt, stream);
-  if (rc) return rc;
+  int rc = NSW_OK;
+  if (x) {
+    rc = nsw_window_partition_sumsq(x, X[0], S1, B, T, H, W, C, s0->ws0, s0->ws1, shapes[0].s0, shapes[0].s1, dt,
+                                    stream);
+    if (rc) return rc;
+  }
   for (int64_t i = 0; i < depth; ++i) {
     const nsw_block_shape* s = shapes + i;
     const nsw_block_params* p = params + i;
-    void* xw = X[i & 1];
+    void* xw = i == 0 && !x ? const_cast<void*>(x0w) : X[i & 1];
+    const float* s1 = i == 0 && !x ? s0w : S1;
     const bool last = i + 1 == depth;
     // K2
-    rc = gemm_qkv_rowscale(xw, p->wqkv_n1, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, S1, nparts, M, C, s->num_heads,
+    rc = gemm_qkv_rowscale(xw, p->wqkv_n1, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, s1, nparts, M, C, s->num_heads,
                            dt, stream);
     if (rc) return rc;
     // K3
@@ -283,4 +292,23 @@ extern "C" int nsw_swin_blocks_forward(const void* x, void* y, const nsw_block_p
     if (rc) return rc;
   }
   return NSW_OK;
+}
+
+extern "C" int nsw_swin_blocks_forward(const void* x, void* y, const nsw_block_params* params,
+                                       const nsw_block_shape* shapes, int64_t depth, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  if (!x) return set_error(NSW_ERR_INVALID, "nsw_swin_blocks_forward: x is null");
+  return blocks_chain(x, nullptr, nullptr, y, params, shapes, depth, workspace, workspace_bytes, stream,
+                      "nsw_swin_blocks_forward");
+}
+
+extern "C" int nsw_swin_blocks_forward_windowed(const void* xw, const float* row_sumsq, void* y,
+                                                const nsw_block_params* params, const nsw_block_shape* shapes,
+                                                int64_t depth, void* workspace, size_t workspace_bytes,
+                                                void* stream) {
+  if (!xw || !row_sumsq) return set_error(NSW_ERR_INVALID, "nsw_swin_blocks_forward_windowed: null input");
+  NSW_CHECK_ARG(((uintptr_t)row_sumsq % 16) == 0, "%s: row_sumsq must be 16-byte aligned",
+                "nsw_swin_blocks_forward_windowed");
+  return blocks_chain(nullptr, xw, row_sumsq, y, params, shapes, depth, workspace, workspace_bytes, stream,
+                      "nsw_swin_blocks_forward_windowed");
 }

@@ -516,9 +516,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   constexpr bool SCAT = EPI == EPI_SCATTER_RESIDUAL;
   constexpr bool REMAP = EPI == EPI_REMAP_RESIDUAL;
   constexpr bool TOK = EPI == EPI_TOKEN_RESIDUAL;
-  constexpr bool RES = EPI == EPI_BIAS_RESIDUAL || SCAT || REMAP || TOK || EPI == EPI_RES_SUMSQ;
+  constexpr bool TOWIN = EPI == EPI_WINDOW_RESIDUAL;
+  constexpr bool RES = EPI == EPI_BIAS_RESIDUAL || SCAT || REMAP || TOK || TOWIN || EPI == EPI_RES_SUMSQ;
   // row sums of squares of the stored rows (optional for the scatter)
-  constexpr bool SUMSQ = SCAT || REMAP || EPI == EPI_RES_SUMSQ;
+  constexpr bool SUMSQ = SCAT || REMAP || TOWIN || EPI == EPI_RES_SUMSQ;
   NSW_WAIT_VMCNT(0);                                  // the copies past the last stage
   NSW_WAIT_LGKMCNT0();
   wg_barrier();                                       // the operand ring is no longer read
@@ -574,7 +575,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
     // so lane l maps the wave's row l once and every copy instruction takes
     // its rows' targets from those lanes (v_readlane) instead of all 32 or
     // 64 lanes of a row evaluating the same map.
-    constexpr bool MAPPED = SCAT || TOK || REMAP;
+    constexpr bool MAPPED = SCAT || TOK || REMAP || TOWIN;
     constexpr int WROWS = ITER * RPI;                 // rows per wave per pass
     static_assert(WROWS <= 64, "one row per lane");
     int lmap = 0;
@@ -582,6 +583,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
       int mm = m0 + prow0 + wave * WROWS + (lane % WROWS);
       mm = mm < M ? mm : M - 1;
       if constexpr (REMAP) lmap = (int)ea.geom.row_of_row_shift(mm, ea.dh, ea.dw);
+      else if constexpr (TOWIN) lmap = (int)ea.geom.row_of_token(mm);
       else lmap = (int)ea.geom.token_of_row(mm);
     }
     auto prefetch = [&](int ib, int slot) {
@@ -878,9 +880,9 @@ int gemm_linear_remap(const void* x, const void* w, const void* bias, const void
   const char* what = "nsw_linear_remap_residual";
   NSW_CHECK_ARG(bias && residual, "%s: bias and residual are required", what);
   NSW_CHECK_ARG(residual != (const void*)y, "%s: residual and y must not alias", what);
-  NSW_CHECK_ARG(map_mode >= 0 && map_mode <= 2, "%s: map_mode must be 0, 1 or 2", what);
+  NSW_CHECK_ARG(map_mode >= 0 && map_mode <= 3, "%s: map_mode must be 0, 1, 2 or 3", what);
   NSW_CHECK_ARG((row_sumsq != nullptr) == (map_mode != 1),
-                "%s: row sums of squares are written for map modes 0 and 2 only, and required there", what);
+                "%s: row sums of squares are written for map modes 0, 2 and 3, and required there", what);
   EpiArgs ea{};
   ea.bias = bias; ea.residual = residual;
   if (map_mode != 0) {
@@ -897,6 +899,7 @@ int gemm_linear_remap(const void* x, const void* w, const void* bias, const void
   if (row_sumsq) NSW_CHECK_ARG(((uintptr_t)row_sumsq % 4) == 0, "%s: row_sumsq must be 4-byte aligned", what);
   if (map_mode == 0) return dispatch_gemm<EPI_RES_SUMSQ>(dtype, x, w, y, M, N, K, ea, stream, what);
   if (map_mode == 1) return dispatch_gemm<EPI_TOKEN_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);
+  if (map_mode == 3) return dispatch_gemm<EPI_WINDOW_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);
   return dispatch_gemm<EPI_REMAP_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);
 }
 

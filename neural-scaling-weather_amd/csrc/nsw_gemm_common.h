@@ -13,6 +13,7 @@ enum Epi {
   EPI_BIAS_GELU = NSW_EPI_BIAS_GELU,
   EPI_BIAS_RESIDUAL = NSW_EPI_BIAS_RESIDUAL,
   EPI_BIAS_GELU_TANH = NSW_EPI_BIAS_GELU_TANH,
+  EPI_WINDOW_RESIDUAL = 10,  // bias, + residual[m], stored at row_of_token(m) (token -> window order), + row sums
   EPI_SCATTER_RESIDUAL = 11, // bias, row m -> token_of_row(m), + skip[token]
   EPI_REMAP_RESIDUAL = 12,   // bias, + residual[m], stored at row_of_row_shift(m), + row sums of squares
   EPI_RES_SUMSQ = 13,        // bias, + residual[m], stored at row m, + row sums of squares

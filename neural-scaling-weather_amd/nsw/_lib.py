@@ -73,6 +73,8 @@ SIGNATURES = {
     "nsw_blocks_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(BlockShape), _i64]),
     "nsw_swin_blocks_forward": (_int, [_vp, _vp, ctypes.POINTER(BlockParams), ctypes.POINTER(BlockShape), _i64,
                                        _vp, ctypes.c_size_t, _vp]),
+    "nsw_swin_blocks_forward_windowed": (_int, [_vp, _vp, _vp, ctypes.POINTER(BlockParams),
+                                                ctypes.POINTER(BlockShape), _i64, _vp, ctypes.c_size_t, _vp]),
     "nsw_window_partition_sumsq": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                           _int, _vp]),
     "nsw_weighted_metrics_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64]),

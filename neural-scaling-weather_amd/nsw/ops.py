@@ -391,8 +391,9 @@ def linear_remap_residual(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, 
     """(y, row_sumsq): y[map(m)] = x[m] . w^T + bias + residual[m] for window
     rows of ``image`` = (B, T, H, W) with ``window_size`` / ``shift_size``:
     map_mode 0 identity, 1 to token order, 2 to the window order of the
-    same image rolled by ``next_shift``; row_sumsq [M, P] fp32 (the stored
-    rows' partial sums of squares, at the stored rows) for modes 0 and 2,
+    same image rolled by ``next_shift``, 3 from token-ordered rows into the
+    window order with ``shift_size``; row_sumsq [M, P] fp32 (the stored
+    rows' partial sums of squares, at the stored rows) for modes 0, 2 and 3,
     None for mode 1."""
     dev = _dev(x, w, bias, residual)
     _same_dtype(x, w, bias, residual)
@@ -459,11 +460,16 @@ def swin_block_forward(x: torch.Tensor, packed: dict, num_heads: int, window_siz
 
 
 def swin_blocks_forward(x: torch.Tensor, packs, num_heads: int, window_size, shifts, eps: Optional[float] = None,
-                        out: Optional[torch.Tensor] = None, gelu_tanh: bool = False) -> torch.Tensor:
+                        out: Optional[torch.Tensor] = None, gelu_tanh: bool = False,
+                        row_sumsq: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The blocks loop ``for blk in blocks: x = blk(x)`` through one C-ABI
     call that keeps the residual stream in window order between blocks.
     ``packs[i]`` is block i's dict of nsw_block_params tensors and must hold
-    the norm-folded ``wqkv_n1`` and ``w1_n2``; ``shifts[i]`` its shift."""
+    the norm-folded ``wqkv_n1`` and ``w1_n2``; ``shifts[i]`` its shift.  With
+    ``row_sumsq`` ([rows, P] fp32, as window_partition_sumsq returns), x holds
+    block 0's input already in block 0's window order (same [B, T, H, W, C]
+    shape, rows in window order) and those are its norm1 sums of squares;
+    the result is in token order either way."""
     packs = list(packs)
     if not packs or len(packs) != len(shifts):
         raise ValueError("swin_blocks_forward: one pack and one shift per block")
@@ -483,8 +489,17 @@ def swin_blocks_forward(x: torch.Tensor, packs, num_heads: int, window_size, shi
         raise ValueError("swin_blocks_forward: malformed block shape")
     ws = workspace(nbytes, dev)
     y = torch.empty_like(x) if out is None else out
-    check(lib().nsw_swin_blocks_forward(x.data_ptr(), y.data_ptr(), params, shapes, depth, ws.data_ptr(),
-                                        ws.numel(), _stream(dev)), "swin_blocks_forward")
+    if row_sumsq is None:
+        check(lib().nsw_swin_blocks_forward(x.data_ptr(), y.data_ptr(), params, shapes, depth, ws.data_ptr(),
+                                            ws.numel(), _stream(dev)), "swin_blocks_forward")
+    else:
+        if row_sumsq.dtype != torch.float32 or not row_sumsq.is_contiguous() or row_sumsq.device != dev:
+            raise ValueError("swin_blocks_forward: row_sumsq must be a contiguous float32 tensor on x's device")
+        if row_sumsq.numel() != (x.numel() // x.shape[-1]) * lib().nsw_row_sumsq_parts(x.shape[-1], dtype_code(x)):
+            raise ValueError("swin_blocks_forward: row_sumsq must be [rows, nsw_row_sumsq_parts(C)]")
+        check(lib().nsw_swin_blocks_forward_windowed(x.data_ptr(), row_sumsq.data_ptr(), y.data_ptr(), params,
+                                                     shapes, depth, ws.data_ptr(), ws.numel(), _stream(dev)),
+              "swin_blocks_forward")
     return y
 
 

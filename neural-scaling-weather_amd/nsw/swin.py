@@ -101,6 +101,22 @@ class Conv2DLayer(nn.Module):
             y = torch_ops.linear_epi(pm, wp, b, residual=residual)
         return y.view(B, T, H // p, W // p, wp.shape[0])
 
+    def tokens_windowed(self, x: torch.Tensor, residual: torch.Tensor, window_size, shift_size,
+                        invariants: Optional[torch.Tensor] = None, frame0: int = 0):
+        """tokens() with the rows stored straight in the window order of the
+        token image rolled by -shift (the first block's order), together with
+        their partial sums of squares: (y [B, T, H/p, W/p, E] holding the
+        window-ordered rows, row_sumsq [rows, P] fp32)."""
+        B, T, C, H, W = x.shape
+        p = self.patch
+        wp, b, Kp = self.packed()
+        if b is None:
+            raise NotImplementedError("the window-order embedding fuses the conv bias and a residual")
+        pm = torch.ops.nsw.patch_im2col(x, p, Kp, wp.dtype, invariants, int(frame0))
+        y, ss = torch.ops.nsw.linear_to_window(pm, wp, b, residual, [B, T, H // p, W // p],
+                                               [int(v) for v in window_size], [int(v) for v in shift_size])
+        return y.view(B, T, H // p, W // p, wp.shape[0]), ss
+
     def forward(self, x):
         """Conv2d semantics: [N, C, H, W] -> [N, E, H // p, W // p] (rows and
         columns beyond the last whole patch are ignored, as Conv2d does)."""
@@ -146,6 +162,17 @@ class PatchEmbedLayer(nn.Module):
         if H != self.h * p or W != self.w * p:
             raise ValueError(f"input extent {(H, W)} does not match the layer's {(self.h * p, self.w * p)}")
         return self.proj.tokens(x, residual=residual, invariants=invariants, frame0=frame0)
+
+    def tokens_windowed(self, x: torch.Tensor, residual: torch.Tensor, window_size, shift_size,
+                        invariants: Optional[torch.Tensor] = None, frame0: int = 0):
+        """tokens() stored in the window order of the first block, with the rows'
+        partial sums of squares (Conv2DLayer.tokens_windowed)."""
+        B, T, C, H, W = x.shape
+        p = self.patch_size
+        if H != self.h * p or W != self.w * p:
+            raise ValueError(f"input extent {(H, W)} does not match the layer's {(self.h * p, self.w * p)}")
+        return self.proj.tokens_windowed(x, residual, window_size, shift_size, invariants=invariants,
+                                         frame0=frame0)
 
     def forward(self, x):
         """Conv2d semantics: [N, C, H, W] -> [N, E, H/p, W/p]."""
@@ -346,18 +373,30 @@ class SwinTransformer(nn.Module):
         [C_inv, H, W] are appended as input channels inside the patch gather,
         frame t is read from slot (t + frame0) mod T of x, and ``out`` receives
         the prediction (any float dtype; e.g. a slot of the input ring)."""
-        y = self.prepare_tokens(x, invariants=invariants, frame0=frame0)
-        y = self.forward_blocks(y)
+        if self._embed_into_chain():
+            # the embedding GEMM stores its rows in block 0's window order with
+            # their norm1 statistics, the chain's own first pass
+            b0 = self.blocks[0]
+            w = self.patch_embed.proj.conv.weight
+            pos = self._pos_tokens(x.shape[0], w.dtype, w.device)
+            yw, ss = self.patch_embed.tokens_windowed(x, pos, b0.window_size, b0.shift_size, invariants=invariants,
+                                                      frame0=frame0)
+            params, shifts, eps, tanh = self._chain_args(yw)
+            y = torch.ops.nsw.swin_blocks_windowed(yw, ss, params, b0.num_heads, [int(v) for v in b0.window_size],
+                                                   shifts, eps, tanh)
+        else:
+            y = self.prepare_tokens(x, invariants=invariants, frame0=frame0)
+            y = self.forward_blocks(y)
         return self._head_last(y, out=out)
 
-    def forward_blocks(self, y: torch.Tensor) -> torch.Tensor:
-        """``for blk in self.blocks: y = blk(y)`` (models/swin.py:307-308),
-        through the window-order chain when ``chain_blocks`` is set."""
-        if not self.chain_blocks or len(self.blocks) == 0:
-            for blk in self.blocks:
-                y = blk(y)
-            return y
-        b0 = self.blocks[0]
+    def _embed_into_chain(self) -> bool:
+        """The embedding writes the chain's window-ordered input when the blocks
+        run as the chain and the patch convolution has the bias that the
+        fused write-out needs."""
+        return (self.chain_blocks and len(self.blocks) > 0 and self.patch_embed.proj.conv.bias is not None)
+
+    def _chain_args(self, y: torch.Tensor):
+        """(params, shifts, eps, gelu_tanh) of the blocks as one chain."""
         for blk in self.blocks:
             blk.check_input(y)
         eps = {blk._eps(y.dtype) for blk in self.blocks}
@@ -368,8 +407,19 @@ class SwinTransformer(nn.Module):
         for blk in self.blocks:
             params += torch_ops.block_param_list(blk.packed(fold_all=True))
             shifts += [int(blk.shift_size[0]), int(blk.shift_size[1])]
-        return torch.ops.nsw.swin_blocks(y, params, b0.num_heads, [int(v) for v in b0.window_size], shifts,
-                                         eps.pop(), tanh.pop())
+        return params, shifts, eps.pop(), tanh.pop()
+
+    def forward_blocks(self, y: torch.Tensor) -> torch.Tensor:
+        """``for blk in self.blocks: y = blk(y)`` (models/swin.py:307-308),
+        through the window-order chain when ``chain_blocks`` is set."""
+        if not self.chain_blocks or len(self.blocks) == 0:
+            for blk in self.blocks:
+                y = blk(y)
+            return y
+        b0 = self.blocks[0]
+        params, shifts, eps, tanh = self._chain_args(y)
+        return torch.ops.nsw.swin_blocks(y, params, b0.num_heads, [int(v) for v in b0.window_size], shifts, eps,
+                                         tanh)
 
 
 class TimeStepper(nn.Module):

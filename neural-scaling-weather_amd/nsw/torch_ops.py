@@ -70,6 +70,27 @@ def _(x, params, num_heads, window_size, shifts, eps, gelu_tanh):
     return torch.empty_like(x, memory_format=torch.contiguous_format)
 
 
+@torch.library.custom_op("nsw::swin_blocks_windowed", mutates_args=())
+def swin_blocks_windowed(xw: torch.Tensor, row_sumsq: torch.Tensor, params: List[Optional[torch.Tensor]],
+                         num_heads: int, window_size: List[int], shifts: List[int], eps: float,
+                         gelu_tanh: bool) -> torch.Tensor:
+    """swin_blocks from block 0's window order: xw [B, T, H, W, C] holding the
+    rows in block 0's window order, row_sumsq their norm1 partial sums."""
+    nb = len(BLOCK_PARAMS)
+    depth = len(shifts) // 2
+    if depth == 0 or len(shifts) != 2 * depth or len(params) != nb * depth:
+        raise ValueError("swin_blocks_windowed: one parameter list and one shift pair per block")
+    packs = [_unpack_block(params[i * nb:(i + 1) * nb]) for i in range(depth)]
+    sh = [(shifts[2 * i], shifts[2 * i + 1]) for i in range(depth)]
+    return ops.swin_blocks_forward(xw.contiguous(), packs, num_heads, tuple(window_size), sh, eps=eps,
+                                   gelu_tanh=gelu_tanh, row_sumsq=row_sumsq.contiguous())
+
+
+@swin_blocks_windowed.register_fake
+def _(xw, row_sumsq, params, num_heads, window_size, shifts, eps, gelu_tanh):
+    return torch.empty_like(xw, memory_format=torch.contiguous_format)
+
+
 # ------------------------------------------------------------ linear / norm ---
 
 @torch.library.custom_op("nsw::linear", mutates_args=())
@@ -83,6 +104,25 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], 
 @linear.register_fake
 def _(x, weight, bias, residual, epilogue):
     return x.new_empty(tuple(x.shape[:-1]) + (weight.shape[0],))
+
+
+@torch.library.custom_op("nsw::linear_to_window", mutates_args=())
+def linear_to_window(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, residual: torch.Tensor,
+                     image: List[int], window_size: List[int], shift_size: List[int]) -> Tuple[torch.Tensor,
+                                                                                               torch.Tensor]:
+    """(y, row_sumsq): token-ordered rows x . weight^T + bias + residual stored
+    in the window order of image (B, T, H, W) rolled by -shift, with the
+    stored rows' partial sums of squares (nsw_linear_remap_residual mode 3)."""
+    return ops.linear_remap_residual(x.contiguous(), weight.contiguous(), bias.contiguous(), residual.contiguous(),
+                                     3, image=tuple(image), window_size=tuple(window_size),
+                                     shift_size=tuple(shift_size))
+
+
+@linear_to_window.register_fake
+def _(x, weight, bias, residual, image, window_size, shift_size):
+    M, N = x.numel() // x.shape[-1], weight.shape[0]
+    P = (N * x.element_size() + 511) // 512
+    return x.new_empty((M, N)), x.new_empty((M, P), dtype=torch.float32)
 
 
 def linear_epi(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,

@@ -213,12 +213,13 @@ def test_qkv_projection_rowscale(device, dtype, tol):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
 def test_linear_remap_residual(device, dtype, mode):
     """nsw_linear_remap_residual: rows of x . w^T + b + residual stored at
-    the identity (0), the token of each window row (1) or that token's row in
-    the window order of another shift (2), with the stored rows' partial sums
-    of squares for modes 0 and 2 (index maps from oracle/index_maps.py)."""
+    the identity (0), the token of each window row (1), that token's row in
+    the window order of another shift (2), or, for token-ordered rows, each
+    token's row in the window order (3), with the stored rows' partial sums
+    of squares for modes 0, 2 and 3 (index maps from oracle/index_maps.py)."""
     from nsw import ops
     from oracle import index_maps
     B, T, H, W, ws, sh, sh2, K, N = 2, 1, 18, 36, (9, 18), (4, 9), (0, 0), 128, 256
@@ -236,6 +237,9 @@ def test_linear_remap_residual(device, dtype, mode):
     tok = torch.from_numpy(index_maps.gather_rows(B, T, H, W, ws[0], ws[1], sh[0], sh[1]))
     if mode == 0:
         dest = torch.arange(M)
+    elif mode == 3:
+        dest = torch.empty(M, dtype=torch.int64)
+        dest[tok] = torch.arange(M)                  # token m -> its window row
     else:
         dest = tok
         if mode == 2:
@@ -252,3 +256,48 @@ def test_linear_remap_residual(device, dtype, mode):
     else:
         es = 4 if dtype == torch.float32 else 2
         torch.testing.assert_close(ss.cpu(), _partial_sumsq(y.cpu(), es), rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_chain_from_window_order(device, dtype):
+    """nsw_swin_blocks_forward_windowed on block 0's window order and norm1
+    sums (as the partition pre-pass writes them) equals the chain from
+    token order bit for bit, and leaves its inputs untouched."""
+    from nsw import ops
+    shifts = [(4, 9), (0, 0), (4, 9)]
+    blocks, _ = make_stack(device, dtype, 1, 18, 36, 128, 2, (9, 18), shifts, seed=12)
+    x = synth.activations((2, 1, 18, 36, 128), seed=13).to(device, dtype)
+    b0 = blocks[0]
+    packs = [b.packed(fold_all=True) for b in blocks]
+    with torch.inference_mode():
+        want = run_chain(blocks, x)
+        xw, ss = ops.window_partition_sumsq(x, b0.window_size, b0.shift_size)
+        xw, ss0 = xw.reshape(x.shape), ss.clone()
+        xw0 = xw.clone()
+        got = ops.swin_blocks_forward(xw, packs, b0.num_heads, b0.window_size, shifts, eps=b0._eps(dtype),
+                                      gelu_tanh=b0.mlp.gelu_tanh, row_sumsq=ss)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(xw, xw0) and torch.equal(ss, ss0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_embedding_into_window_order(device, dtype):
+    """The embedding GEMM's window-order write-out (map mode 3) stores the
+    rows the partition pre-pass makes of its token-order output, and their
+    sums of squares up to summation order."""
+    from nsw import ops, torch_ops
+    B, T, H, W, ws, sh, K, N = 1, 1, 18, 36, (9, 18), (0, 0), 128, 256
+    M = B * T * H * W
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(M, K, generator=g).to(dtype).to(device)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(dtype).to(device)
+    b = torch.randn(N, generator=g).to(dtype).to(device)
+    r = torch.randn(M, N, generator=g).to(dtype).to(device)
+    with torch.inference_mode():
+        tok = torch_ops.linear_epi(x, w, b, residual=r)
+        want_w, want_ss = ops.window_partition_sumsq(tok.view(B, T, H, W, N), ws, sh)
+        got_w, got_ss = torch.ops.nsw.linear_to_window(x, w, b, r, [B, T, H, W], list(ws), list(sh))
+    torch.cuda.synchronize()
+    assert torch.equal(got_w.reshape(-1), want_w.reshape(-1))
+    torch.testing.assert_close(got_ss, want_ss, rtol=2e-6, atol=1e-6)

@@ -13,7 +13,7 @@ import torch
 import nsw
 from nsw import torch_ops
 
-OPS = ["swin_block", "swin_blocks", "linear", "rms_norm", "layer_norm", "qkv_projection", "window_attention",
+OPS = ["swin_block", "swin_blocks", "swin_blocks_windowed", "linear_to_window", "linear", "rms_norm", "layer_norm", "qkv_projection", "window_attention",
        "window_partition", "window_reverse", "roll_hw", "roll_window_partition", "window_reverse_roll",
        "patch_im2col", "unpatchify", "head_unpatchify", "weighted_metrics"]
 
@@ -33,6 +33,11 @@ def test_shape_functions():
     x = meta(2, 1, 18, 36, 128)
     assert n.swin_block(x, P, 2, [9, 18], [4, 9], 1e-7, False).shape == x.shape
     assert n.swin_blocks(x, P * 3, 2, [9, 18], [0, 0, 4, 9, 0, 0], 1e-7, False).shape == x.shape
+    assert n.swin_blocks_windowed(x, meta(648 * 2, 1, dtype=torch.float32), P * 2, 2, [9, 18], [0, 0, 4, 9],
+                                  1e-7, False).shape == x.shape
+    yw, ss = n.linear_to_window(meta(648, 1152), meta(1024, 1152), meta(1024), meta(648, 1024), [1, 1, 18, 36],
+                                [9, 18], [0, 0])
+    assert yw.shape == (648, 1024) and ss.shape == (648, 4) and ss.dtype == torch.float32
     y = n.linear(meta(7, 5, 64), meta(96, 64), meta(96), None, 1)
     assert y.shape == (7, 5, 96) and y.dtype == torch.bfloat16
     assert n.rms_norm(meta(3, 64), meta(64), 1e-7).shape == (3, 64)
@@ -107,7 +112,8 @@ def test_model_traces_into_one_graph():
     torch.compile(model, backend=cap, fullgraph=True)(torch.randn(1, 1, C, H, W))
     assert len(cap.graphs) == 1
     t = targets(cap.graphs[0])
-    assert count(t, "swin_blocks") == 1          # the blocks as one window-order chain
+    assert count(t, "swin_blocks_windowed") == 1  # the blocks as one window-order chain
+    assert count(t, "linear_to_window") == 1      # fed by the embedding in block 0's window order
     assert count(t, "patch_im2col") == 2         # the image and the coordinate embedding
     assert count(t, "head_unpatchify") == 1       # the head GEMM with the head layout fused
     model.chain_blocks = False
