@@ -6,7 +6,8 @@
 // LDS: a workgroup owns R consecutive patch rows, reads the image side along
 // its contiguous rows (p consecutive pixels per patch row segment, adjacent
 // patches adjacent in memory) and the patch-matrix side as whole contiguous
-// rows with 16-byte vectors.
+// rows with 16-byte vectors.  Float images with p = 2 or 4 (the models')
+// take im2col_dma_kernel instead: image runs copied straight into LDS.
 //
 // Patch matrix: row (b, t, i, j) of [B*T*h*w, Kp], column k = (c*p + u)*p + v
 // (the flattening order of a Conv2d weight [E, C, p, p]) holds
@@ -25,6 +26,9 @@
 namespace nsw {
 
 constexpr int MODEL_LDS = 64 * 1024;   // dynamic LDS per workgroup (at most)
+#ifndef IM2COL_DMA_NB
+#define IM2COL_DMA_NB 64                // 1 KB runs per workgroup of the direct-to-LDS patch matrix
+#endif
 // unpatchify's tile: smaller tiles, more workgroups per CU (measured at
 // config 3: 24 KB tiles 70 us against 77 us with 64 KB)
 constexpr int UNPATCH_LDS = 24 * 1024;
@@ -132,6 +136,100 @@ __global__ __launch_bounds__(256) void im2col_kernel(const TX* __restrict__ x, c
   for (int e = tid; e < rows * vpr; e += 256) {
     const int r = e / vpr, cc = e - r * vpr;
     orow[e] = *reinterpret_cast<const Vt*>(tile + r * KS + cc * V);
+  }
+}
+
+// Patch matrix from float images with p = 2 or 4 (the models' patch sizes)
+// through direct-to-LDS copies, so that a workgroup's loads are all in
+// flight at once without register staging.  A workgroup owns TG = 256 / p
+// consecutive patches (j0 ..) of patch row i of one frame and CG = NB / p
+// channels (cg*CG ..): LDS block d = c' p + u (1 KB) receives the TG patches'
+// run of image row i p + u of channel c' -- 64 lanes x 16 bytes, lane l
+// loading the run's 16-byte chunk l ^ s(c', u), so that chunk q sits at
+// slot q ^ s.  s(c', u) is the index of the patch-matrix row chunk that
+// run's values land in, so the 16 lanes that write 16 consecutive chunks of
+// one patch row read 16 distinct 16-byte slots (all 64 banks).  Chunks past
+// the image row's end re-read its last chunk (never stored).  Then each
+// thread writes 16-byte chunks of the patch rows (CG channels' p*p columns
+// per row, the last group also the zero columns up to Kp).
+template <int P, typename TO>
+__device__ __forceinline__ int im2col_swz(int cl, int u) {
+  return (((cl * P + u) * P * (int)sizeof(TO)) >> 4) & 15;
+}
+
+template <typename TO, int P, int NB>
+__global__ __launch_bounds__(256) void im2col_dma_kernel(const float* __restrict__ x, const float* __restrict__ inv,
+                                                         int Cx, int Cinv, int T, int H, int W, int frame0, int Kp,
+                                                         int ncg, int ntg, TO* __restrict__ out) {
+  constexpr int CG = NB / P;                 // channels per workgroup
+  constexpr int TG = 64 * 4 / P;             // patches per workgroup: one 1 KB run per image row
+  constexpr int V = 16 / (int)sizeof(TO);    // patch-matrix elements per 16-byte chunk
+  constexpr int CPR = CG * P * P / V;        // chunks per patch-row segment
+  static_assert(V % P == 0 && NB % 4 == 0, "im2col_dma_kernel layout");
+  __shared__ __attribute__((aligned(1024))) char smem[NB * 1024];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = H / P, w = W / P, C = Cx + Cinv, Kc = C * P * P;
+  int item = blockIdx.x;                     // channel group fastest, then patch group, patch row, frame
+  const int cg = item % ncg;
+  item /= ncg;
+  const int jg = item % ntg;
+  item /= ntg;
+  const int i = item % h;
+  const int bt = item / h;                   // b * T + t
+  const int t = bt % T, b = bt / T;
+  int ts = t + frame0;
+  if (ts >= T) ts -= T;
+  const int64_t HW = (int64_t)H * W;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+#pragma unroll
+  for (int j = 0; j < NB / 4; ++j) {
+    const int d = wave * (NB / 4) + j;
+    const int cl = d / P, u = d - cl * P;
+    int c = cg * CG + cl;
+    c = c < C ? c : C - 1;                   // past C: a valid plane, never stored
+    const float* plane = c < Cx ? x + ((int64_t)(b * T + ts) * Cx + c) * HW : inv + (int64_t)(c - Cx) * HW;
+    int x0 = jg * TG * P + (lane ^ im2col_swz<P, TO>(cl, u)) * 4;
+    x0 = x0 + 4 <= W ? x0 : W - 4;
+    dma16(make_rsrc(plane, (uint32_t)(HW * 4)), lds0 + (uint32_t)d * 1024u, (uint32_t)(((i * P + u) * W + x0) * 4),
+          0u);
+  }
+  NSW_WAIT_VMCNT(0);
+  __syncthreads();
+
+  const int k0 = cg * CG * P * P;
+  for (int e = tid; e < TG * CPR; e += 256) {
+    const int tt = e / CPR, ch = e - tt * CPR;
+    const int j = jg * TG + tt;
+    const int kk = k0 + ch * V;
+    if (j >= w || kk >= Kp) continue;
+    TO v[V];
+#pragma unroll
+    for (int r = 0; r < V / P; ++r) {
+      const int kl = ch * V + r * P;         // column within the group: c' p^2 + u p
+      const int cl = kl / (P * P), u = (kl / P) % P;
+      float f[P];
+      if (k0 + kl < Kc) {
+        const int slot = ((tt * P) >> 2) ^ im2col_swz<P, TO>(cl, u);
+        const char* src = smem + (cl * P + u) * 1024 + slot * 16 + ((tt * P * 4) & 15);
+        if constexpr (P == 4) {
+          const f32x4 q = *reinterpret_cast<const f32x4*>(src);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) f[k] = q[k];
+        } else {
+          const float2 q = *reinterpret_cast<const float2*>(src);
+          f[0] = q.x;
+          f[1] = q.y;
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < P; ++k) f[k] = 0.f;   // zero columns Kc .. Kp-1
+      }
+#pragma unroll
+      for (int k = 0; k < P; ++k) v[r * P + k] = from_f32<TO>(f[k]);
+    }
+    const int64_t m = ((int64_t)bt * h + i) * w + j;
+    *reinterpret_cast<u32x4*>(out + m * Kp + kk) = __builtin_bit_cast(u32x4, v);
   }
 }
 
@@ -290,6 +388,31 @@ extern "C" int nsw_patch_im2col(const void* x, const void* inv, int64_t B, int64
   NSW_CHECK_ARG(B * T * C_x * H * W < (1LL << 40) && H * W < (1LL << 31), "%s: too large", what);
   const int64_t M = B * T * (H / p) * (W / p);
   const size_t es = dtype_size(out_dtype);
+  // float images with p = 2 or 4: the direct-to-LDS kernel
+  if (x_dtype == NSW_DTYPE_F32 && (p == 2 || p == 4) && W % 4 == 0 && ((uintptr_t)x % 16) == 0 &&
+      (inv == nullptr || ((uintptr_t)inv % 16) == 0)) {
+    constexpr int NB = IM2COL_DMA_NB;
+    const int CG = NB / (int)p, TG = 256 / (int)p;
+    const int64_t C = C_x + C_inv;
+    const int64_t ncg = (C + CG - 1) / CG, ntg = (W / p + TG - 1) / TG;
+    const int64_t items = B * T * (H / p) * ntg * ncg;
+    if (ncg * CG * p * p >= Kp && items < (1LL << 31)) {
+      hipStream_t st = (hipStream_t)stream;
+#define NSW_IM2COL_DMA(TO, P)                                                                                  \
+  hipLaunchKernelGGL((im2col_dma_kernel<TO, P, NB>), dim3((unsigned)items), dim3(256), 0, st, (const float*)x, \
+                     (const float*)inv, (int)C_x, (int)C_inv, (int)T, (int)H, (int)W, (int)frame0, (int)Kp,   \
+                     (int)ncg, (int)ntg, (TO*)out)
+      if (out_dtype == NSW_DTYPE_BF16) {
+        if (p == 4) NSW_IM2COL_DMA(bf16, 4); else NSW_IM2COL_DMA(bf16, 2);
+      } else if (out_dtype == NSW_DTYPE_F32) {
+        if (p == 4) NSW_IM2COL_DMA(float, 4); else NSW_IM2COL_DMA(float, 2);
+      } else {
+        return set_error(NSW_ERR_INVALID, "%s: unknown output dtype %d", what, out_dtype);
+      }
+#undef NSW_IM2COL_DMA
+      return check_launch(what);
+    }
+  }
   const int row_bytes = (int)((Kp + V) * es);
   NSW_CHECK_ARG(row_bytes <= MODEL_LDS, "%s: Kp=%lld too large for one LDS row", what, (long long)Kp);
   const int R = rows_per_wg(MODEL_LDS, row_bytes);

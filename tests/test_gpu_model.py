@@ -36,7 +36,10 @@ def rel_l2(a, b):
 @pytest.mark.parametrize("xd,od", [(torch.float32, torch.float32), (torch.float32, torch.bfloat16),
                                    (torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32)])
 @pytest.mark.parametrize("B,T,Cx,Ci,H,W,p,frame0", [(2, 2, 3, 0, 8, 12, 4, 0), (1, 3, 5, 2, 12, 16, 2, 1),
-                                                    (1, 1, 70, 0, 32, 64, 4, 0), (2, 2, 4, 1, 6, 9, 3, 1)])
+                                                    (1, 1, 70, 0, 32, 64, 4, 0), (2, 2, 4, 1, 6, 9, 3, 1),
+                                                    (1, 1, 5, 0, 8, 16, 2, 0),      # a chunk straddles C*p*p
+                                                    (1, 1, 3, 1, 4, 1440, 4, 0),    # 6 patch groups, last partial
+                                                    (1, 2, 5, 0, 2, 1440, 2, 1)])   # p = 2, 128-patch groups
 def test_patch_im2col_bit_exact(device, xd, od, B, T, Cx, Ci, H, W, p, frame0):
     import nsw
     g = torch.Generator().manual_seed(B * 7 + Cx)
@@ -53,6 +56,23 @@ def test_patch_im2col_bit_exact(device, xd, od, B, T, Cx, Ci, H, W, p, frame0):
         src = torch.cat([src, inv.view(1, 1, Ci, H, W).expand(B, T, Ci, H, W)], dim=2)
     want = mr.im2col_bruteforce(src.reshape(B * T, Cx + Ci, H, W).float(), p).to(od)
     assert got.shape == (B * T * (H // p) * (W // p), Kp)
+    assert torch.equal(got[:, :K], want)
+    assert torch.all(got[:, K:] == 0)
+
+
+@pytest.mark.parametrize("p,od", [(4, torch.bfloat16), (2, torch.bfloat16), (4, torch.float32)])
+def test_patch_im2col_full_size(device, p, od):
+    """The patch matrix of a [1, 1, 70, 720, 1440] float image (configs 3-5)
+    against the view / permute form of the same layout (the brute-force
+    oracle's order, checked on small shapes above)."""
+    import nsw
+    C, H, W = 70, 720, 1440
+    x = torch.randn(1, 1, C, H, W, generator=torch.Generator().manual_seed(p))
+    K = C * p * p
+    Kp = (K + 63) // 64 * 64
+    got = nsw.ops.patch_im2col(x.to(device), p, Kp, od).cpu()
+    h, w = H // p, W // p
+    want = x.view(C, h, p, w, p).permute(1, 3, 0, 2, 4).reshape(h * w, K).to(od)
     assert torch.equal(got[:, :K], want)
     assert torch.all(got[:, K:] == 0)
 
