@@ -356,11 +356,14 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   // Tiles of one XCD run in groups of GROUP_M row blocks x all column blocks,
   // column-major inside the group, so that the tiles in flight on an XCD
   // share both their row panels and their weight panels in its L2.
+  // (ea.group_m row blocks when set: 4 for the QKV projection, measured 3%
+  // faster there, 2% slower for fc1)
+  const int GM = ea.group_m > 0 ? ea.group_m : GROUP_M;
   const int tile = xcd_remap(blockIdx.x, MT * NT);
-  const int group = tile / (GROUP_M * NT);
-  const int gm0 = group * GROUP_M;
-  const int gsz = MT - gm0 < GROUP_M ? MT - gm0 : GROUP_M;
-  const int tin = tile - group * GROUP_M * NT;
+  const int group = tile / (GM * NT);
+  const int gm0 = group * GM;
+  const int gsz = MT - gm0 < GM ? MT - gm0 : GM;
+  const int tin = tile - group * GM * NT;
   const int mt = gm0 + tin % gsz, nt = tin / gsz;
   const int m0 = mt * BM, n0 = nt * BN;
 
@@ -756,6 +759,7 @@ int gemm_qkv(const void* x, const void* wqkv, const void* bqkv, const void* qn_w
   NSW_CHECK_ARG(bqkv && qn_w && kn_w, "%s: bias and norm weights are required", what);
   EpiArgs ea{};
   ea.bias = bqkv; ea.qn_w = qn_w; ea.kn_w = kn_w; ea.eps = eps; ea.C = (int)C;
+  ea.group_m = 4;
   if (hd == 64) return dispatch_gemm<EPI_QKV_HN64>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
   if (hd == 32) return dispatch_gemm<EPI_QKV_HN32>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
   return dispatch_gemm<EPI_QKV_HN16>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
@@ -832,6 +836,7 @@ int gemm_qkv_norm_gather(const void* x, const void* wqkv_n, const void* bqkv, co
   NSW_CHECK_ARG(x != (const void*)qkv, "%s: x and qkv must not alias", what);
   EpiArgs ea{};
   ea.bias = bqkv; ea.qn_w = qn_w; ea.kn_w = kn_w; ea.eps = eps; ea.C = (int)C;
+  ea.group_m = 4;
   ea.geom = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
   const int64_t M = B * T * H * W;
   if (hd == 64)
@@ -860,6 +865,7 @@ int gemm_qkv_rowscale(const void* x, const void* wqkv_n, const void* bqkv, const
                 "%s: row_sumsq [M, nparts] (16-byte aligned) is required", what);
   EpiArgs ea{};
   ea.bias = bqkv; ea.qn_w = qn_w; ea.kn_w = kn_w; ea.eps = eps; ea.C = (int)C;
+  ea.group_m = 4;
   ea.row_sumsq = const_cast<float*>(row_sumsq);
   ea.nparts = (int)nparts;
   if (hd == 64) return dispatch_gemm<EPI_QKV_HN64, PRE_ROWSCALE>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);

@@ -60,6 +60,7 @@ struct EpiArgs {
   float* row_sumsq;
   int nparts;
   int dh, dw;   // EPI_REMAP_RESIDUAL: shift differences of geom.row_of_row_shift
+  int group_m;  // row blocks per XCD tile group (0: GROUP_M)
   // EPI_UNPATCH: image [B, 1, img_C, img_H, img_W], frames img_bstride
   // elements apart, in float (img_f32) or the GEMM's dtype; patch img_p
   void* img;
