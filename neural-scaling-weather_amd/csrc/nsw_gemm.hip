@@ -356,8 +356,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   // Tiles of one XCD run in groups of GROUP_M row blocks x all column blocks,
   // column-major inside the group, so that the tiles in flight on an XCD
   // share both their row panels and their weight panels in its L2.
-  // (ea.group_m row blocks when set: 4 for the QKV projection, measured 3%
-  // faster there, 2% slower for fc1)
+  // (ea.group_m row blocks when set: 4 for the QKV projection and 16 for
+  // proj, each measured 1.5-3% faster there; fc1 is fastest at 8)
   const int GM = ea.group_m > 0 ? ea.group_m : GROUP_M;
   const int tile = xcd_remap(blockIdx.x, MT * NT);
   const int group = tile / (GM * NT);
@@ -785,6 +785,7 @@ int gemm_proj_scatter(const void* o, const void* wproj, const void* bproj, const
   ea.geom = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
   ea.row_sumsq = row_sumsq;
   ea.nparts = (int)sumsq_parts(C, dtype);
+  ea.group_m = 16;   // proj's 4 column blocks: 16-row-block groups measured 2.5% faster than 8
   return dispatch_gemm<EPI_SCATTER_RESIDUAL>(dtype, o, wproj, y, B * T * H * W, C, C, ea, stream, what);
 }
 
@@ -903,7 +904,10 @@ int gemm_linear_remap(const void* x, const void* w, const void* bias, const void
   ea.row_sumsq = row_sumsq;
   ea.nparts = (int)sumsq_parts(N, dtype);
   if (row_sumsq) NSW_CHECK_ARG(((uintptr_t)row_sumsq % 4) == 0, "%s: row_sumsq must be 4-byte aligned", what);
-  if (map_mode == 0) return dispatch_gemm<EPI_RES_SUMSQ>(dtype, x, w, y, M, N, K, ea, stream, what);
+  if (map_mode == 0) {
+    ea.group_m = N <= 1024 ? 16 : 0;   // proj-shaped (few column blocks): 16-row-block groups
+    return dispatch_gemm<EPI_RES_SUMSQ>(dtype, x, w, y, M, N, K, ea, stream, what);
+  }
   if (map_mode == 1) return dispatch_gemm<EPI_TOKEN_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);
   if (map_mode == 3) return dispatch_gemm<EPI_WINDOW_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);
   return dispatch_gemm<EPI_REMAP_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);
