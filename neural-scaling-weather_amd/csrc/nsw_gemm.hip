@@ -731,8 +731,15 @@ static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t
                 "%s: x, w, y and residual must be 16-byte aligned", what);
   NSW_CHECK_ARG(((M + BM - 1) / BM) * ((N + BN - 1) / BN) < (1LL << 31), "%s: too many tiles", what);
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  EpiArgs eg = ea;
+  if constexpr (EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_GELU_TANH) {
+    // the MLP's first GEMM: tile groups of ~128 tiles (8 row blocks x 16
+    // column blocks at config 2, 16 x 8 at config 4: each measured 5% faster
+    // than the other height on its shape)
+    if (eg.group_m == 0) eg.group_m = (int)std::max<int64_t>(8, std::min<int64_t>(32, 128 / ((N + BN - 1) / BN)));
+  }
   hipLaunchKernelGGL((gemm_kernel<T, EPI, PRE>), dim3((unsigned)tiles), dim3(NW * 64), 0, st, (const T*)x, (const T*)w,
-                     (T*)y, (int)M, (int)N, (int)K, ea);
+                     (T*)y, (int)M, (int)N, (int)K, eg);
   return check_launch(what);
 }
 
