@@ -15,6 +15,10 @@ The line also carries
   "gemm_vs_hipblaslt": the block's four GEMM shapes without epilogue, this
               library's GEMM against torch.matmul (hipBLASLt), same operands;
   "config4":  the config-4 block and one forward of the depth-8 p2 model;
+  "achievable": this box's own peaks, a 1 GiB device copy (HBM) and an
+              8192^3 hipBLASLt GEMM in the block's dtype (MFMA); every
+              kernel entry and the roofline also give frac_achievable, the
+              fraction of those beside the fraction of the spec peaks;
 and, unless --no-model is given,
   "forecast": config 3, one SwinTransformer forward (p4, e1024, depth 16,
               16 heads, window 9x18, 70 channels, 720x1440, bf16) = ms per
@@ -300,6 +304,13 @@ def main():
 
     # ----------------------------------------- metrics kernel (config 5 step)
     kern["metrics_unnorm"] = metrics_timing(dev, args.steps, args.warmup)
+    # ------------------------------- achievable peaks of this box, and fractions
+    ach = achievable_peaks(dev, dtype, args.steps, args.warmup)
+    out["achievable"] = ach
+    for k in kern.values():
+        ref = ach["mfma_tflops"] if k["bound"] == "mfma" else ach["hbm_copy_GBs"]
+        k["frac_achievable"] = round(k["achieved"] / ref, 4)
+    roofline["frac_achievable"] = kern[dom]["frac_achievable"]
     # ------------------------------------------------ GEMMs against hipBLASLt
     if not args.no_gemm_compare and args.config in ("c2", "c2u"):
         out["gemm_vs_hipblaslt"] = gemm_compare(dev, M, C, 4 * C, args.steps, args.warmup)
@@ -454,6 +465,28 @@ def metrics_timing(dev, steps, warmup):
             "frac": round(ach / PEAK_HBM_GBS, 4), "bytes": nbytes,
             "workload": "config 5 per-step metrics: [1,1,70,720,1440] fp32 prediction and target, "
                         "unnormalise + weighted RMSE + ACC (two launches: partial sums, final)"}
+
+
+def achievable_peaks(dev, dtype, steps, warmup):
+    """What this box reaches on its own: a 1 GiB device-to-device copy (HBM,
+    bytes read + written) and an 8192^3 torch.matmul in the block's dtype
+    (hipBLASLt), the references of the per-kernel frac_achievable."""
+    import torch
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    t_copy = timed(lambda: dst.copy_(src), steps, warmup)
+    del src, dst
+    N = 8192
+    g = torch.Generator(device=dev).manual_seed(4102)
+    a = torch.randn(N, N, generator=g, device=dev).to(dtype)
+    b = torch.randn(N, N, generator=g, device=dev).to(dtype)
+    t_mm = timed(lambda: torch.matmul(a, b), steps, warmup)
+    del a, b
+    return {"hbm_copy_GBs": round(2 * n * 4 / (t_copy * 1e-3) / 1e9, 1),
+            "mfma_tflops": round(2.0 * N ** 3 / (t_mm * 1e-3) / 1e12, 1),
+            "copy": "1 GiB fp32 tensor copy_ (read + write bytes)",
+            "gemm": f"torch.matmul {N}x{N}x{N} {str(dtype).replace('torch.', '')} (hipBLASLt)"}
 
 
 def gemm_compare(dev, M, C, Hm, steps, warmup):
