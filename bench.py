@@ -15,6 +15,8 @@ The line also carries
   "gemm_vs_hipblaslt": the block's four GEMM shapes without epilogue, this
               library's GEMM against torch.matmul (hipBLASLt), same operands;
   "config4":  the config-4 block and one forward of the depth-8 p2 model;
+  "shard":    one GPU's share of config 2 split 2-way in longitude (the
+              block on 180 x 180 tokens), time per token against the full block;
   "achievable": this box's own peaks, a 1 GiB device copy (HBM) and an
               8192^3 hipBLASLt GEMM in the block's dtype (MFMA); every
               kernel entry and the roofline also give frac_achievable, the
@@ -319,6 +321,7 @@ def main():
         del st
         torch.cuda.empty_cache()
         out["config4"] = config4_section(dev, args.steps, args.warmup, args.model_steps)
+        out["shard"] = shard_section(dev, args.steps, args.warmup, M, ms_step)
 
     # ------------------------------------------------- config 3 / config 5
     if not args.no_model:
@@ -513,6 +516,27 @@ def gemm_compare(dev, M, C, Hm, steps, warmup):
                      "max_abs_diff": diff}
         del x, w, wt, a, b
     return res
+
+
+def shard_section(dev, steps, warmup, M_full, ms_full):
+    """One GPU's share of config 2 under a 2-way longitude split (sp2 = 2):
+    the shifted block on 180 x 180 tokens (200 windows), the kernels one GPU
+    would run at that shard's shape; the halo exchange of the roll is not
+    part of it (one GPU, local cyclic roll)."""
+    import torch
+    import nsw
+    B, T, H, W, C, heads, ws, shift = 1, 1, 180, 180, 1024, 16, (9, 18), (4, 9)
+    torch.manual_seed(5002)
+    blk = nsw.Block(C, heads, (H, W), ws, T, shift_size=shift).to(device=dev, dtype=torch.bfloat16).eval()
+    x = torch.randn(B, T, H, W, C, device=dev).to(torch.bfloat16)
+    with torch.inference_mode():
+        ms = timed(lambda: blk(x), steps, warmup)
+    del blk, x
+    M = B * T * H * W
+    return {"workload": "config 2 split 2-way in longitude (sp2 = 2): shifted block on 180 x 180 tokens, "
+                        "C=1024, 16 heads, window 9x18 (200 windows), one GPU's shard, no halo exchange",
+            "tokens": M, "ms": round(ms, 4), "tokens_per_s": round(M / (ms * 1e-3), 1),
+            "per_token_vs_full": round((ms / M) / (ms_full / M_full), 4)}
 
 
 def config4_section(dev, steps, warmup, model_steps):
