@@ -8,7 +8,8 @@ through the fused C-ABI call nsw_swin_block_forward.  Prints one JSON line:
 tokens/s over K timed steps (inputs resident in HBM), the roofline of the
 dominant kernel from HIP events on the launch stream, the per-kernel
 breakdown, and a CPU baseline (the fp32 oracle on the host cores, on a
-bounded sample of the same workload).  One GPU only.
+bounded sample of the same workload; with the config-1 block and one
+config-3 step assembled from its timed parts beside it).  One GPU only.
 
 The line also carries
   "kernels.metrics_unnorm": the config-5 per-step RMSE/ACC reduction (HBM);
@@ -728,6 +729,7 @@ def cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, target_s):
             break
     med = statistics.median(times)
     toks = B * T * Hs * W
+    extra = cpu_extra_cases(p, xs, heads, ws, shift, med, nbands / nb)
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -741,7 +743,58 @@ def cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, target_s):
             "kind": "port",
             "sample": f"fp32 oracle block (oracle/swin_ref.py, eager torch) on {nb} of {nbands} latitude bands "
                       f"({Hs}x{W} tokens = {toks}, C={C}), median of {len(times)} runs "
-                      f"({med:.2f} s each); cpu: {cpu_model}"}
+                      f"({med:.2f} s each); cpu: {cpu_model}",
+            **extra}
+
+
+def cpu_extra_cases(p, xs, heads, ws, shift, shifted_s, scale):
+    """The other CPU figures of the measurement spec, on the same cores: the
+    config-1 block (fp32, 90x180 tokens, C=192, 6 heads, median of 5) and one
+    config-3 step assembled from its parts -- the patch embedding
+    (Conv2d p4 of the [70, 720, 1440] input + the coordinate embedding) and
+    the head (Linear 1024 -> 70*16 + unpatchify), each timed once, plus 8
+    shifted and 8 unshifted config-2 blocks (the config-3 blocks are config 2's
+    shape), the unshifted one timed once on the same sample; ``scale`` lifts a
+    sample of latitude bands to the whole image."""
+    import torch
+    from oracle import model_ref, swin_ref, synth
+    out = {}
+    p1 = synth.block_params(192, 6, seed=1001)
+    x1 = synth.activations((1, 1, 90, 180, 192), seed=1002)
+    swin_ref.block_forward(x1, p1, 6, (9, 18), (4, 9))
+    t = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        swin_ref.block_forward(x1, p1, 6, (9, 18), (4, 9))
+        t.append(time.perf_counter() - t0)
+    out["c1_block_ms"] = round(1e3 * statistics.median(t), 2)
+    t0 = time.perf_counter()
+    swin_ref.block_forward(xs, p, heads, ws, (0, 0))
+    unshifted_s = time.perf_counter() - t0
+    E, p4, ch = 1024, 4, 70
+    g = torch.Generator().manual_seed(3001)
+    x = torch.randn(1, 1, ch, 720, 1440, generator=g)
+    pe_w = synth.trunc_normal((E, ch, p4, p4), 0.02, g)
+    pos_w = synth.trunc_normal((E, 4, p4, p4), 0.02, g)
+    head_w = synth.trunc_normal((ch * p4 * p4, E), 0.02, g)
+    lat = torch.linspace(90, -90, 721)[:-1]
+    lon = torch.linspace(0, 360, 1441)[:-1]
+    coords = model_ref.model_coords(model_ref.spatial_coords(lat, lon), 1)
+    t0 = time.perf_counter()
+    pos = model_ref.pos_tokens(coords, pos_w, torch.zeros(E), p4)
+    tok = model_ref.prepare_tokens(x, pe_w, torch.zeros(E), p4, pos)
+    embed_s = time.perf_counter() - t0
+    del x, pos
+    t0 = time.perf_counter()
+    model_ref.forward_head(tok, head_w, p4, ch)
+    head_s = time.perf_counter() - t0
+    step = embed_s + head_s + 8 * scale * (shifted_s + unshifted_s)
+    out["c3_step"] = {"s": round(step, 2), "embed_s": round(embed_s, 3), "head_s": round(head_s, 3),
+                      "block_shifted_s": round(scale * shifted_s, 3),
+                      "block_unshifted_s": round(scale * unshifted_s, 3),
+                      "note": "embed + head timed once at full size, + 8 shifted and 8 unshifted "
+                              "config-2 blocks (fp32 oracle, eager torch)"}
+    return out
 
 
 if __name__ == "__main__":
