@@ -69,6 +69,7 @@ BF16_CASES = [
     (1, 1, 90, 180, 192, 6, (9, 18), (4, 9)),
     (1, 2, 18, 36, 128, 2, (9, 18), (4, 9)),
     (1, 1, 360, 720, 512, 8, (9, 18), (4, 9)),     # config 4 (p2: 259,200 tokens, 1,600 windows)
+    (1, 1, 180, 180, 1024, 16, (9, 18), (4, 9)),   # one GPU's share of config 2 split 2-way in longitude
 ]
 
 
