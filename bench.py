@@ -623,17 +623,40 @@ def model_sections(dev, steps, warmup, with_rollout=True, with_block_calls=True)
         e1.record(stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
-        # stage split (spin kernel first: see the per-kernel loop of the block)
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-        torch.cuda._sleep(SPIN_CYCLES)
-        ev[0].record(stream)
-        tok = model.prepare_tokens(x)
-        ev[1].record(stream)
-        tok = model.forward_blocks(tok)
-        ev[2].record(stream)
-        model._head_last(tok)
-        ev[3].record(stream)
-        torch.cuda.synchronize()
+        # stage split of the same forward path (model.forward: the embedding
+        # into block 0's window order, the window-order chain, the fused
+        # head), averaged over `steps` passes with events between the stages
+        # and a spin kernel first (see the per-kernel loop of the block).  The
+        # chain's argument lists are built once beforehand: in the pipelined
+        # steps above the host builds them while the GPU runs the previous step.
+        split = [0.0, 0.0, 0.0]
+        chain = model._embed_into_chain()
+        if chain:
+            b0 = model.blocks[0]
+            w_pe = model.patch_embed.proj.conv.weight
+            pos = model._pos_tokens(x.shape[0], w_pe.dtype, w_pe.device)
+            params, shifts, eps, tanh = model._chain_args(model.patch_embed.tokens_windowed(
+                x, pos, b0.window_size, b0.shift_size)[0])
+        for _ in range(steps):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            torch.cuda._sleep(SPIN_CYCLES)
+            ev[0].record(stream)
+            if chain:
+                yw, ss = model.patch_embed.tokens_windowed(x, pos, b0.window_size, b0.shift_size)
+                ev[1].record(stream)
+                tok = torch.ops.nsw.swin_blocks_windowed(yw, ss, params, b0.num_heads,
+                                                         [int(v) for v in b0.window_size], shifts, eps, tanh)
+                del yw, ss
+            else:
+                tok = model.prepare_tokens(x)
+                ev[1].record(stream)
+                tok = model.forward_blocks(tok)
+            ev[2].record(stream)
+            model._head_last(tok)
+            ev[3].record(stream)
+            torch.cuda.synchronize()
+            for i in range(3):
+                split[i] += ev[i].elapsed_time(ev[i + 1]) / steps
         if not torch.isfinite(yb.float()).all():
             raise RuntimeError("non-finite forecast")
         # the same step with one fused call per block (no window-order chain)
@@ -655,8 +678,7 @@ def model_sections(dev, steps, warmup, with_rollout=True, with_block_calls=True)
         "ms_per_step": round(ms, 3), "steps": steps, "tflop_per_step": round(step_flops / 1e12, 3),
         "tflops_achieved": round(step_flops / (ms * 1e-3) / 1e12, 1),
         "tokens_per_s": round(tokens / (ms * 1e-3), 1),
-        "embed_ms": round(ev[0].elapsed_time(ev[1]), 3), "blocks_ms": round(ev[1].elapsed_time(ev[2]), 3),
-        "head_ms": round(ev[2].elapsed_time(ev[3]), 3),
+        "embed_ms": round(split[0], 3), "blocks_ms": round(split[1], 3), "head_ms": round(split[2], 3),
         "ms_per_step_block_calls": None if ms_per_block is None else round(ms_per_block, 3),
     }
     del tok, yb
