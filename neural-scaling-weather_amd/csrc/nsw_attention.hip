@@ -821,6 +821,8 @@ static int launch_f32(const AttnArgs& a, int64_t items, hipStream_t st) {
 template <typename T>
 static int launch_scalar(const AttnArgs& a, int hd, int64_t grid, hipStream_t st) {
   switch (hd) {
+    case 4: hipLaunchKernelGGL((attn_scalar_kernel<T, 4>), dim3((unsigned)grid), dim3(256), 0, st, a); return 0;
+    case 8: hipLaunchKernelGGL((attn_scalar_kernel<T, 8>), dim3((unsigned)grid), dim3(256), 0, st, a); return 0;
     case 16: hipLaunchKernelGGL((attn_scalar_kernel<T, 16>), dim3((unsigned)grid), dim3(256), 0, st, a); return 0;
     case 32: hipLaunchKernelGGL((attn_scalar_kernel<T, 32>), dim3((unsigned)grid), dim3(256), 0, st, a); return 0;
     case 64: hipLaunchKernelGGL((attn_scalar_kernel<T, 64>), dim3((unsigned)grid), dim3(256), 0, st, a); return 0;
@@ -877,7 +879,7 @@ extern "C" int nsw_window_attention(const void* qkv, void* o, const float* mask,
   } else if (dtype == NSW_DTYPE_F32) {
     if (hd == 64 && a.mask_mode != MASK_TENSOR && launch_f32(a, grid, st) == 0) return check_launch(what);
     if (launch_scalar<float>(a, hd, grid, st) != 0)
-      return set_error(NSW_ERR_UNSUPPORTED, "%s: head_dim=%d unsupported (16, 32, 64, 128)", what, hd);
+      return set_error(NSW_ERR_UNSUPPORTED, "%s: head_dim=%d unsupported (4, 8, 16, 32, 64, 128)", what, hd);
   } else {
     return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, dtype);
   }

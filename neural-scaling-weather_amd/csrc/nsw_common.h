@@ -130,6 +130,13 @@ __device__ __forceinline__ float rows4_sum(float x) {
   return c + d;
 }
 
+// Sum over the pair of 16-lane rows (lanes l, l^16) only.
+__device__ __forceinline__ float rows2_sum(float x) {
+  float a = x, b = x;
+  permlane16_swap(a, b);
+  return a + b;
+}
+
 // Sum over the 16 lanes of a DPP row (lanes 16r .. 16r+15), on every lane:
 // rotations by 8, 4, 2, 1 within the row.
 __device__ __forceinline__ float row16_sum(float x) {

@@ -403,17 +403,21 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   }
 
   // per-head RMSNorm (QKV epilogue): a head is HDQ/16 consecutive 16-column
-  // blocks inside one of the q / k / v regions (C % 64 == 0, HDQ | 64), so
-  // whether a head is normalised is uniform across the wave
-  constexpr int NBH = HDQ > 0 ? HDQ / 16 : 1;   // blocks per head
-  constexpr int NHW = NB / NBH;                 // heads per wave tile
+  // blocks inside one of the q / k / v regions (C % 16 == 0 and HDQ | C), so
+  // whether a head is normalised is uniform across its lanes.  Head dims 4
+  // and 8 put 4 / 2 heads in one 16-column block: a lane's 4 columns are a
+  // whole head (4) or half of one, the other half in the lane 16 apart (8);
+  // then the flags below are kept per block (NBH = 1, "heads" = blocks).
+  constexpr int NBH = HDQ >= 16 ? HDQ / 16 : 1;  // blocks per head
+  constexpr int HSP = HDQ >= 16 ? HDQ : 16;      // columns per flag slot
+  constexpr int NHW = NB / NBH;                  // flag slots per wave tile
   bool normed[NHW];
   int nwreg[NHW];                               // 0: q weights, 1: k weights
   float nwv[NB][4];
   if constexpr (HDQ > 0) {
 #pragma unroll
     for (int h = 0; h < NHW; ++h) {
-      const int c0 = nw0 + h * HDQ;
+      const int c0 = nw0 + h * HSP;
       const int region = c0 / ea.C;  // 0: q, 1: k, 2: v
       normed[h] = region < 2 && c0 < N;
       nwreg[h] = region == 0 ? 0 : 1;
@@ -473,7 +477,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
         for (int b = 0; b < NBH; ++b)
 #pragma unroll
           for (int r = 0; r < 4; ++r) sh = fmaf(v[h * NBH + b][r], v[h * NBH + b][r], sh);
-        ss[h] = rows4_sum(sh);
+        if constexpr (HDQ >= 16) ss[h] = rows4_sum(sh);
+        else if constexpr (HDQ == 8) ss[h] = rows2_sum(sh);
+        else ss[h] = sh;
       }
 #pragma unroll
       for (int h = 0; h < NHW; ++h) {
@@ -553,7 +559,8 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
       for (int h = 0; h < NHW; ++h)
 #pragma unroll
         for (int b = 0; b < NBH; ++b) {
-          const f32x4 w4 = *reinterpret_cast<const f32x4*>(prm + PRM_NW + nwreg[h] * HDQ + b * 16 + fg * 4);
+          const int dcol = HDQ >= 16 ? b * 16 + fg * 4 : (fg * 4) % HDQ;   // column within the head
+          const f32x4 w4 = *reinterpret_cast<const f32x4*>(prm + PRM_NW + nwreg[h] * HDQ + dcol);
 #pragma unroll
           for (int r = 0; r < 4; ++r) nwv[h * NBH + b][r] = w4[r];
         }
@@ -760,15 +767,17 @@ int gemm_qkv(const void* x, const void* wqkv, const void* bqkv, const void* qn_w
   NSW_CHECK_ARG(num_heads > 0 && C % num_heads == 0, "%s: C=%lld not divisible by num_heads=%lld", what,
                 (long long)C, (long long)num_heads);
   const int64_t hd = C / num_heads;
-  NSW_CHECK_ARG(C % 64 == 0, "%s: C=%lld must be a multiple of 64", what, (long long)C);
-  NSW_CHECK_ARG(hd == 16 || hd == 32 || hd == 64, "%s: head_dim=%lld unsupported (16, 32, 64)", what,
-                (long long)hd);
+  NSW_CHECK_ARG(C % 16 == 0, "%s: C=%lld must be a multiple of 16", what, (long long)C);
+  NSW_CHECK_ARG(hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64,
+                "%s: head_dim=%lld unsupported (4, 8, 16, 32, 64)", what, (long long)hd);
   NSW_CHECK_ARG(bqkv && qn_w && kn_w, "%s: bias and norm weights are required", what);
   EpiArgs ea{};
   ea.bias = bqkv; ea.qn_w = qn_w; ea.kn_w = kn_w; ea.eps = eps; ea.C = (int)C;
   ea.group_m = 4;
   if (hd == 64) return dispatch_gemm<EPI_QKV_HN64>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
   if (hd == 32) return dispatch_gemm<EPI_QKV_HN32>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
+  if (hd == 8) return dispatch_gemm<EPI_QKV_HN8>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
+  if (hd == 4) return dispatch_gemm<EPI_QKV_HN4>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
   return dispatch_gemm<EPI_QKV_HN16>(dtype, x, wqkv, qkv, M, 3 * C, C, ea, stream, what);
 }
 
@@ -837,9 +846,9 @@ int gemm_qkv_norm_gather(const void* x, const void* wqkv_n, const void* bqkv, co
   NSW_CHECK_ARG(num_heads > 0 && C % num_heads == 0, "%s: C=%lld not divisible by num_heads=%lld", what,
                 (long long)C, (long long)num_heads);
   const int64_t hd = C / num_heads;
-  NSW_CHECK_ARG(C % 64 == 0, "%s: C=%lld must be a multiple of 64", what, (long long)C);
-  NSW_CHECK_ARG(hd == 16 || hd == 32 || hd == 64, "%s: head_dim=%lld unsupported (16, 32, 64)", what,
-                (long long)hd);
+  NSW_CHECK_ARG(C % 16 == 0, "%s: C=%lld must be a multiple of 16", what, (long long)C);
+  NSW_CHECK_ARG(hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64,
+                "%s: head_dim=%lld unsupported (4, 8, 16, 32, 64)", what, (long long)hd);
   NSW_CHECK_ARG(bqkv && qn_w && kn_w, "%s: bias and norm weights are required", what);
   NSW_CHECK_ARG(x != (const void*)qkv, "%s: x and qkv must not alias", what);
   EpiArgs ea{};
@@ -851,6 +860,8 @@ int gemm_qkv_norm_gather(const void* x, const void* wqkv_n, const void* bqkv, co
     return dispatch_gemm<EPI_QKV_HN64, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
   if (hd == 32)
     return dispatch_gemm<EPI_QKV_HN32, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+  if (hd == 8) return dispatch_gemm<EPI_QKV_HN8, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+  if (hd == 4) return dispatch_gemm<EPI_QKV_HN4, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
   return dispatch_gemm<EPI_QKV_HN16, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
 }
 
@@ -865,9 +876,9 @@ int gemm_qkv_rowscale(const void* x, const void* wqkv_n, const void* bqkv, const
   NSW_CHECK_ARG(num_heads > 0 && C % num_heads == 0, "%s: C=%lld not divisible by num_heads=%lld", what,
                 (long long)C, (long long)num_heads);
   const int64_t hd = C / num_heads;
-  NSW_CHECK_ARG(C % 64 == 0, "%s: C=%lld must be a multiple of 64", what, (long long)C);
-  NSW_CHECK_ARG(hd == 16 || hd == 32 || hd == 64, "%s: head_dim=%lld unsupported (16, 32, 64)", what,
-                (long long)hd);
+  NSW_CHECK_ARG(C % 16 == 0, "%s: C=%lld must be a multiple of 16", what, (long long)C);
+  NSW_CHECK_ARG(hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64,
+                "%s: head_dim=%lld unsupported (4, 8, 16, 32, 64)", what, (long long)hd);
   NSW_CHECK_ARG(bqkv && qn_w && kn_w, "%s: bias and norm weights are required", what);
   NSW_CHECK_ARG(row_sumsq != nullptr && nparts > 0 && nparts <= 4096 && ((uintptr_t)row_sumsq % 16) == 0,
                 "%s: row_sumsq [M, nparts] (16-byte aligned) is required", what);
@@ -878,6 +889,8 @@ int gemm_qkv_rowscale(const void* x, const void* wqkv_n, const void* bqkv, const
   ea.nparts = (int)nparts;
   if (hd == 64) return dispatch_gemm<EPI_QKV_HN64, PRE_ROWSCALE>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
   if (hd == 32) return dispatch_gemm<EPI_QKV_HN32, PRE_ROWSCALE>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+  if (hd == 8) return dispatch_gemm<EPI_QKV_HN8, PRE_ROWSCALE>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
+  if (hd == 4) return dispatch_gemm<EPI_QKV_HN4, PRE_ROWSCALE>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
   return dispatch_gemm<EPI_QKV_HN16, PRE_ROWSCALE>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
 }
 

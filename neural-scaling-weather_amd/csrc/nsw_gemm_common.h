@@ -22,7 +22,9 @@ enum Epi {
                              // pixel (dy, dx) of the token's patch in image plane c
   EPI_QKV_HN16 = 16,         // bias, then per-head RMSNorm of the q and k
   EPI_QKV_HN32 = 32,         // columns, for head dims 16 / 32 / 64
-  EPI_QKV_HN64 = 64
+  EPI_QKV_HN64 = 64,
+  EPI_QKV_HN4 = 68,          // the same for head dims 4 and 8: a head inside
+  EPI_QKV_HN8 = 72           // one 16-column block (4 / 8 of its columns)
 };
 
 // Operand-side fusions (template parameter PRE):
@@ -44,7 +46,8 @@ enum Pre { PRE_NONE = 0, PRE_ROWNORM = 1, PRE_ROWNORM_GATHER = 2, PRE_ROWSCALE =
 constexpr bool pre_sums_in_loop(int pre) { return pre == PRE_ROWNORM || pre == PRE_ROWNORM_GATHER; }
 
 constexpr int qkv_head_dim(int epi) {
-  return (epi == EPI_QKV_HN16 || epi == EPI_QKV_HN32 || epi == EPI_QKV_HN64) ? epi : 0;
+  return (epi == EPI_QKV_HN16 || epi == EPI_QKV_HN32 || epi == EPI_QKV_HN64) ? epi
+         : epi == EPI_QKV_HN4 ? 4 : epi == EPI_QKV_HN8 ? 8 : 0;
 }
 
 struct EpiArgs {

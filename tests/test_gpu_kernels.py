@@ -110,7 +110,8 @@ def test_linear_epilogues(device, dtype, M, N, K, epi):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("M,C,heads", [(64800, 1024, 16), (16200, 192, 6), (500, 128, 8), (100, 64, 1)])
+@pytest.mark.parametrize("M,C,heads", [(64800, 1024, 16), (16200, 192, 6), (500, 128, 8), (100, 64, 1),
+                                      (500, 64, 16), (700, 128, 16)])   # head dims 4 and 8
 def test_qkv_projection_headnorm(device, dtype, M, C, heads):
     from nsw import ops
     hd = C // heads
@@ -128,6 +129,26 @@ def test_qkv_projection_headnorm(device, dtype, M, C, heads):
     k = ref.rms_norm(k.reshape(M, heads, hd), kn.float(), eps).reshape(M, C)
     want = torch.cat([q, k, v], -1)
     assert rel_l2(got, want) < TOL[dtype]
+
+
+def test_qkv_projection_headnorm_c32_fp32(device):
+    """C = 32 with 8 heads (head dim 4), the width of the reference's model
+    test (tests/test_all.py); fp32 only (bf16 GEMMs take K in multiples of 64)."""
+    from nsw import ops
+    M, C, heads, hd = 777, 32, 8, 4
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(M, C, generator=g)
+    w = synth.trunc_normal((3 * C, C), 0.02, g)
+    b = 0.1 * torch.randn(3 * C, generator=g)
+    qn = 1 + 0.2 * torch.randn(hd, generator=g)
+    kn = 1 + 0.2 * torch.randn(hd, generator=g)
+    eps = torch.finfo(torch.float32).eps
+    got = ops.qkv_projection(x.to(device), w.to(device), b.to(device), qn.to(device), kn.to(device), heads, eps)
+    y = ref_linear(x, w, device) + b
+    q, k, v = y.split(C, dim=-1)
+    q = ref.rms_norm(q.reshape(M, heads, hd), qn, eps).reshape(M, C)
+    k = ref.rms_norm(k.reshape(M, heads, hd), kn, eps).reshape(M, C)
+    assert rel_l2(got, torch.cat([q, k, v], -1)) < TOL[torch.float32]
 
 
 def attention_oracle(qkv, heads, scale, mask):
@@ -152,6 +173,8 @@ ATTN_CASES = [
     (1, 1, 16, 32, 64, 2, (4, 8), (2, 4)),
     (1, 1, 9, 18, 128, 2, (9, 18), (0, 0)),
     (3, 1, 18, 36, 320, 5, (9, 18), (4, 9)),
+    (1, 2, 18, 36, 64, 16, (9, 18), (4, 9)),       # head dim 4 (the reference's test model: e32 / 8 heads)
+    (2, 1, 18, 36, 64, 8, (9, 18), (4, 9)),        # head dim 8
 ]
 
 
