@@ -15,11 +15,13 @@ The line also carries
   "kernels.metrics_unnorm": the config-5 per-step RMSE/ACC reduction (HBM);
   "gemm_vs_hipblaslt": the block's four GEMM shapes without epilogue, this
               library's GEMM against torch.matmul (hipBLASLt), same operands;
-  "config4":  the config-4 block and one forward of the depth-8 p2 model;
+  "config4":  the config-4 block (with its per-kernel breakdown) and one
+              forward of the depth-8 p2 model;
   "shard":    one GPU's share of config 2 split 2-way in longitude (the
               block on 180 x 180 tokens), time per token against the full block;
-  "achievable": this box's own peaks, a 1 GiB device copy (HBM) and an
-              8192^3 hipBLASLt GEMM in the block's dtype (MFMA); every
+  "achievable": this box's own peaks, the better of a 1 GiB read-only pass
+              and a 1 GiB device copy (HBM), and the fastest hipBLASLt GEMM
+              of an 8192^3 product and the block's four shapes (MFMA); every
               kernel entry and the roofline also give frac_achievable, the
               fraction of those beside the fraction of the spec peaks;
 and, unless --no-model is given,
@@ -29,8 +31,12 @@ and, unless --no-model is given,
               blocks as one window-order chain), and the same step with one
               fused call per block (ms_per_step_block_calls);
   "rollout":  config 5, 8 autoregressive steps of the config-3 model with
-              per-step latitude-weighted RMSE and ACC (nsw.Rollout), bf16
-              against the same weights in fp32: per-step drift.
+              per-step latitude-weighted RMSE and ACC (nsw.Rollout) in bf16
+              and through this library's fp32 path: per-step drift against
+              the fp32 oracle rollout of the same weights and inputs, whose
+              per-step metrics tests/test_gpu_fullsize.py records in
+              tests/golden/rollout_c5_fp32_oracle.json (bench.py does not run
+              the oracle outside its CPU-baseline leg).
 Inputs there are seeded Gaussian-filtered, per-channel standardised fields
 (sigma = 8 px), standing in for ERA5.
 
@@ -168,6 +174,91 @@ def main():
         if not torch.isfinite(y.float()).all():
             raise RuntimeError("non-finite block output")
 
+        kern, same = block_kernels(blk, x, y, (B, T, H, W, C, heads, ws, shift, dtype), args.norms, args.steps,
+                                   args.warmup)
+    fl = block_flops(B, T, H, W, C, heads, ws)
+    peak_f = PEAK_BF16_TFLOPS if dtype == torch.bfloat16 else PEAK_F32_TFLOPS
+    names = list(kern)
+    dom = max(names, key=lambda n: kern[n]["ms"])
+    d = kern[dom]
+    traffic = None
+    tf_path = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
+    if os.path.exists(tf_path):
+        with open(tf_path) as f:
+            traffic = json.load(f).get(dom)
+    roofline = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"],
+                "peak": peak_f if d["bound"] == "mfma" else PEAK_HBM_GBS, "unit": d["unit"],
+                "frac": d["frac"], "traffic": traffic}
+
+    total_flops = sum(fl.values())
+    out = {
+        "metric": METRIC,
+        "value": round(M / (ms_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dts,
+        "data": "synthetic (N(0,1) activations, reference trunc-normal(0.02) weights)",
+        "config": {"workload": desc, "tokens": M, "block_tflop": round(total_flops / 1e12, 4),
+                   "block_tflops_achieved": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
+                   "wall_s_timed": round(wall, 4), "ops_path_equals_fused": bool(same),
+                   "block_launches": len(names), "norms": args.norms},
+        "roofline": roofline,
+        "kernels": kern,
+    }
+
+    # ----------------------------------------- metrics kernel (config 5 step)
+    kern["metrics_unnorm"] = metrics_timing(dev, args.steps, args.warmup)
+    # ------------------------------------------------ GEMMs against hipBLASLt
+    if not args.no_gemm_compare and args.config in ("c2", "c2u"):
+        out["gemm_vs_hipblaslt"] = gemm_compare(dev, M, C, 4 * C, args.steps, args.warmup)
+    # ------------------------------- achievable peaks of this box, and fractions
+    ach = achievable_peaks(dev, dtype, args.steps, args.warmup, out.get("gemm_vs_hipblaslt"))
+    out["achievable"] = ach
+    for k in kern.values():
+        ref = ach["mfma_tflops"] if k["bound"] == "mfma" else ach["hbm_GBs"]
+        k["frac_achievable"] = round(k["achieved"] / ref, 4)
+    roofline["frac_achievable"] = kern[dom]["frac_achievable"]
+    # ------------------------------------------------------------ config 4
+    if not args.no_config4 and args.config in ("c2", "c2u"):
+        torch.cuda.empty_cache()
+        out["config4"] = config4_section(dev, args.steps, args.warmup, args.model_steps)
+        for k in out["config4"]["block_kernels"].values():
+            k["frac_achievable"] = round(k["achieved"] / (ach["mfma_tflops"] if k["bound"] == "mfma"
+                                                          else ach["hbm_GBs"]), 4)
+        out["shard"] = shard_section(dev, args.steps, args.warmup, M, ms_step)
+
+    # ------------------------------------------------- config 3 / config 5
+    if not args.no_model:
+        del y
+        torch.cuda.empty_cache()
+        out["forecast"], rollout = model_sections(dev, args.model_steps, args.warmup, not args.no_rollout,
+                                                  not args.no_block_calls)
+        if rollout is not None:
+            out["rollout"] = rollout
+
+    # ----------------------------------------------------------- CPU baseline
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+def block_kernels(blk, x, y_fused, cfg, norms, steps, warmup):
+    """The block's kernels launched one op at a time (the same kernels as the
+    fused call) with HIP events between them on the launch stream: per-kernel
+    ms, achieved rate and fraction of the binding spec peak.  Returns
+    (kernels, whether the op-by-op output equals the fused call's)."""
+    import torch
+    from nsw import _lib, ops
+    B, T, H, W, C, heads, ws, shift, dtype = cfg
+    M = B * T * H * W
+    stream = torch.cuda.current_stream(x.device)
+    with torch.inference_mode():
         # ---------------------------------------------- per-kernel breakdown
         # the same kernels, launched one op at a time with HIP events between
         # them on the launch stream
@@ -222,7 +313,7 @@ def main():
         def k_fc2():
             st["y"] = ops.linear(st["u"], pk["w2"], pk["b2"], residual=st["h1"])
 
-        if args.norms == "window":
+        if norms == "window":
             seq = [("partition_sumsq", k_part), ("qkv_rowscale", k_qkv_rs), ("attention", k_attn),
                    ("proj_sumsq", k_proj_id), ("fc1_rowscale", k_fc1_rs), ("fc2_to_tokens", k_fc2_tok)]
         else:
@@ -232,7 +323,7 @@ def main():
             seq += [("fc2", k_fc2)]
         names = [n for n, _ in seq]
         times = {n: [] for n in names}
-        for it in range(args.warmup + args.steps):
+        for it in range(warmup + steps):
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
             # a short spin kernel ahead of the first event keeps the GPU busy
             # while the host enqueues the first op, so that op's interval
@@ -243,11 +334,10 @@ def main():
                 fn()
                 ev[i + 1].record(stream)
             torch.cuda.synchronize()
-            if it >= args.warmup:
+            if it >= warmup:
                 for i, n in enumerate(names):
                     times[n].append(ev[i].elapsed_time(ev[i + 1]))
-        y2 = st["y"]
-        same = torch.equal(y2, y)
+        same = torch.equal(st["y"], y_fused)
 
     es = 2 if dtype == torch.bfloat16 else 4
     A = M * C * es
@@ -272,85 +362,42 @@ def main():
             ach = units / t / 1e9
             kern[n] = {"ms": round(t * 1e3, 4), "bound": "hbm", "achieved": round(ach, 1), "unit": "GB/s",
                        "frac": round(ach / PEAK_HBM_GBS, 4)}
-    dom = max(names, key=lambda n: kern[n]["ms"])
-    d = kern[dom]
-    traffic = None
-    tf_path = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
-    if os.path.exists(tf_path):
-        with open(tf_path) as f:
-            traffic = json.load(f).get(dom)
-    roofline = {"kernel": dom, "bound": d["bound"], "achieved": d["achieved"],
-                "peak": peak_f if d["bound"] == "mfma" else PEAK_HBM_GBS, "unit": d["unit"],
-                "frac": d["frac"], "traffic": traffic}
+    return kern, same
 
-    total_flops = sum(fl.values())
-    out = {
-        "metric": METRIC,
-        "value": round(M / (ms_step * 1e-3), 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": dts,
-        "data": "synthetic (N(0,1) activations, reference trunc-normal(0.02) weights)",
-        "config": {"workload": desc, "tokens": M, "block_tflop": round(total_flops / 1e12, 4),
-                   "block_tflops_achieved": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
-                   "wall_s_timed": round(wall, 4), "ops_path_equals_fused": bool(same),
-                   "block_launches": len(names), "norms": args.norms},
-        "roofline": roofline,
-        "kernels": kern,
-    }
 
-    # ----------------------------------------- metrics kernel (config 5 step)
-    kern["metrics_unnorm"] = metrics_timing(dev, args.steps, args.warmup)
-    # ------------------------------- achievable peaks of this box, and fractions
-    ach = achievable_peaks(dev, dtype, args.steps, args.warmup)
-    out["achievable"] = ach
-    for k in kern.values():
-        ref = ach["mfma_tflops"] if k["bound"] == "mfma" else ach["hbm_copy_GBs"]
-        k["frac_achievable"] = round(k["achieved"] / ref, 4)
-    roofline["frac_achievable"] = kern[dom]["frac_achievable"]
-    # ------------------------------------------------ GEMMs against hipBLASLt
-    if not args.no_gemm_compare and args.config in ("c2", "c2u"):
-        out["gemm_vs_hipblaslt"] = gemm_compare(dev, M, C, 4 * C, args.steps, args.warmup)
-    # ------------------------------------------------------------ config 4
-    if not args.no_config4 and args.config in ("c2", "c2u"):
-        del st
-        torch.cuda.empty_cache()
-        out["config4"] = config4_section(dev, args.steps, args.warmup, args.model_steps)
-        out["shard"] = shard_section(dev, args.steps, args.warmup, M, ms_step)
+CALIB_BYTES = 256 << 20
+CALIB_LAUNCHES = 5
 
-    # ------------------------------------------------- config 3 / config 5
-    if not args.no_model:
-        del y, y2
-        torch.cuda.empty_cache()
-        out["forecast"], rollout = model_sections(dev, args.model_steps, args.warmup, not args.no_rollout,
-                                                  not args.no_block_calls)
-        if rollout is not None:
-            out["rollout"] = rollout
 
-    # ----------------------------------------------------------- CPU baseline
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(blk, B, T, H, W, C, heads, ws, shift, args.cpu_seconds)
-    print(json.dumps(out), flush=True)
+def traffic_minimum(config):
+    """Algorithmic HBM bytes per launch of each block kernel (each operand
+    read once, each output written once; weights and row statistics
+    included): a calibrated counter figure below it is impossible."""
+    B, T, H, W, C, heads, ws, shift, dts, desc = CONFIGS[config]
+    es = 2 if dts == "bf16" else 4
+    M = B * T * H * W
+    A = M * C * es
+    wb = C * C * es                       # one C x C weight
+    ss = M * ((C * es + 511) // 512) * 4  # row partial sums of squares
+    return {"gather_norm1": 2 * A, "partition_sumsq": 2 * A + ss, "qkv": A + 3 * wb + 3 * A,
+            "qkv_rowscale": A + ss + 3 * wb + 3 * A, "attention": 4 * A,
+            "proj_scatter_sumsq": 3 * A + wb + ss, "proj_sumsq": 3 * A + wb + ss,
+            "fc1_rowscale": A + ss + 4 * wb + 4 * A, "fc2": 4 * A + 4 * wb + 2 * A,
+            "fc2_to_tokens": 4 * A + 4 * wb + 2 * A, "metrics_unnorm": 2 * 70 * 720 * 1440 * 4}
 
 
 def copy_calibration():
-    """A plain 256 MiB device-to-device copy, 5 launches: its FETCH_SIZE /
-    WRITE_SIZE per dispatch divided by the bytes it moves is the factor that
-    turns those counters into HBM bytes for the other kernels of the same
-    profiled run."""
+    """A plain 256 MiB device-to-device copy, 5 launches, before any other
+    work: its FETCH_SIZE / WRITE_SIZE per dispatch divided by the bytes it
+    moves is the factor that turns those counters into HBM bytes for the
+    other kernels of the same profiled run."""
     import torch
-    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+    src = torch.empty(CALIB_BYTES, dtype=torch.uint8, device="cuda:0").fill_(1)
     dst = torch.empty_like(src)
-    for _ in range(5):
+    for _ in range(CALIB_LAUNCHES):
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_calibration_bytes": src.numel(), "launches": 5}), flush=True)
+    print(json.dumps({"copy_calibration_bytes": src.numel(), "launches": CALIB_LAUNCHES}), flush=True)
     del src, dst
     torch.cuda.empty_cache()
 
@@ -391,37 +438,55 @@ def traffic_summary(fetch_dir, write_dir, config):
     import glob
 
     def load(d, counter):
-        acc = {}
+        acc, copies = {}, []
         for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             with open(path) as f:
                 for r in csv.DictReader(f):
                     if r["Counter_Name"] != counter:
                         continue
                     n = trace_name(r["Kernel_Name"])
-                    if n is not None:
-                        acc.setdefault(n, []).append((int(r["Grid_Size"]), float(r["Counter_Value"]) * 1024.0))
-        # the calibration copies are the largest copy dispatches (torch's other
-        # small copies use the same blit kernel)
-        if "copy_calibration" in acc:
-            gmax = max(g for g, _ in acc["copy_calibration"])
-            acc["copy_calibration"] = [(g, v) for g, v in acc["copy_calibration"] if g == gmax]
-        return {k: sum(v for _, v in vs) / len(vs) for k, vs in acc.items()}
+                    v = float(r["Counter_Value"]) * 1024.0
+                    if n == "copy_calibration":
+                        copies.append((int(r["Dispatch_Id"]), v))
+                    elif n is not None:
+                        acc.setdefault(n, []).append(v)
+        # the calibration copies are the first CALIB_LAUNCHES blit-copy
+        # dispatches of the run (copy_calibration runs before any other work;
+        # later copies -- the 1 GiB achievable-peak copy, torch's small ones --
+        # use the same blit kernel and grid, so neither size nor grid tells
+        # them apart); they must agree with each other
+        copies.sort()
+        cal = [v for _, v in copies[:CALIB_LAUNCHES]]
+        if len(cal) < CALIB_LAUNCHES:
+            raise SystemExit(f"{counter}: the run holds no calibration copy: profile 'bench.py --copy-calibration ...'")
+        if max(cal) > 1.02 * min(cal):
+            raise SystemExit(f"{counter}: the first {CALIB_LAUNCHES} copies disagree ({min(cal):.4g}..{max(cal):.4g} B):"
+                             " they are not the calibration copies")
+        out = {k: sum(vs) / len(vs) for k, vs in acc.items()}
+        out["copy_calibration"] = sum(cal) / len(cal)
+        return out
 
     fetch, write = load(fetch_dir, "FETCH_SIZE"), load(write_dir, "WRITE_SIZE")
-    if "copy_calibration" not in fetch or "copy_calibration" not in write:
-        raise SystemExit("the runs hold no calibration copy: profile 'bench.py --copy-calibration ...'")
-    nbytes = float(256 << 20)
+    nbytes = float(CALIB_BYTES)
     kf, kw = fetch["copy_calibration"] / nbytes, write["copy_calibration"] / nbytes
+    minimum = traffic_minimum(config)
     out = {}
     rows = []
     for n in sorted(set(fetch) & set(write)):
         if n == "copy_calibration":
             continue
         f, w = fetch[n] / kf, write[n] / kw
+        lo = minimum.get(n)
+        if lo is not None and f + w < 0.98 * lo:
+            raise SystemExit(f"{n}: calibrated traffic {(f + w) / 1e6:.1f} MB is below the kernel's algorithmic "
+                             f"minimum {lo / 1e6:.1f} MB: the calibration is wrong")
         out[n] = int(round(f + w))
-        rows.append(f"| {n} | {f / 1e6:.1f} | {w / 1e6:.1f} | {(f + w) / 1e6:.1f} |")
+        ratio = "" if lo is None else f"{(f + w) / lo:.2f}"
+        rows.append(f"| {n} | {f / 1e6:.1f} | {w / 1e6:.1f} | {(f + w) / 1e6:.1f} | "
+                    f"{'' if lo is None else f'{lo / 1e6:.1f}'} | {ratio} |")
     print(f"calibration (same runs): FETCH_SIZE reads {kf:.4f} x and WRITE_SIZE {kw:.4f} x the copy's bytes")
-    print("| kernel | fetch (MB) | write (MB) | total (MB) |\n|---|---|---|---|")
+    print("| kernel | fetch (MB) | write (MB) | total (MB) | algorithmic (MB) | total / algorithmic |\n"
+          "|---|---|---|---|---|---|")
     print("\n".join(rows))
     out["_calibration"] = {"fetch_factor": round(kf, 4), "write_factor": round(kw, 4)}
     with open(os.path.join(ROOT, "profiles", f"traffic_{config}.json"), "w") as fh:
@@ -471,13 +536,17 @@ def metrics_timing(dev, steps, warmup):
                         "unnormalise + weighted RMSE + ACC (two launches: partial sums, final)"}
 
 
-def achievable_peaks(dev, dtype, steps, warmup):
-    """What this box reaches on its own: a 1 GiB device-to-device copy (HBM,
-    bytes read + written) and an 8192^3 torch.matmul in the block's dtype
-    (hipBLASLt), the references of the per-kernel frac_achievable."""
+def achievable_peaks(dev, dtype, steps, warmup, gemms=None):
+    """What this box reaches on its own, the references of the per-kernel
+    frac_achievable: HBM, the better of a read-only pass (torch.sum over
+    1 GiB) and a 1 GiB device-to-device copy (bytes read + written); MFMA,
+    the fastest of an 8192^3 torch.matmul in the block's dtype and the
+    block's own four GEMM shapes through torch.matmul (``gemms``, the
+    gemm_vs_hipblaslt leg), all hipBLASLt."""
     import torch
     n = 1 << 28
     src = torch.ones(n, dtype=torch.float32, device=dev)
+    t_read = timed(lambda: src.sum(), steps, warmup)
     dst = torch.empty_like(src)
     t_copy = timed(lambda: dst.copy_(src), steps, warmup)
     del src, dst
@@ -487,10 +556,17 @@ def achievable_peaks(dev, dtype, steps, warmup):
     b = torch.randn(N, N, generator=g, device=dev).to(dtype)
     t_mm = timed(lambda: torch.matmul(a, b), steps, warmup)
     del a, b
-    return {"hbm_copy_GBs": round(2 * n * 4 / (t_copy * 1e-3) / 1e9, 1),
-            "mfma_tflops": round(2.0 * N ** 3 / (t_mm * 1e-3) / 1e12, 1),
-            "copy": "1 GiB fp32 tensor copy_ (read + write bytes)",
-            "gemm": f"torch.matmul {N}x{N}x{N} {str(dtype).replace('torch.', '')} (hipBLASLt)"}
+    read_gbs = n * 4 / (t_read * 1e-3) / 1e9
+    copy_gbs = 2 * n * 4 / (t_copy * 1e-3) / 1e9
+    mm = {f"matmul {N}^3": 2.0 * N ** 3 / (t_mm * 1e-3) / 1e12}
+    for name, r in (gemms or {}).items():
+        mm[f"{name} shape"] = r["hipblaslt_tflops"]
+    best = max(mm, key=mm.get)
+    return {"hbm_GBs": round(max(read_gbs, copy_gbs), 1), "hbm_read_GBs": round(read_gbs, 1),
+            "hbm_copy_GBs": round(copy_gbs, 1), "mfma_tflops": round(mm[best], 1),
+            "mfma_source": f"hipBLASLt {best} ({str(dtype).replace('torch.', '')})",
+            "hbm": "max of torch.sum over 1 GiB fp32 (read bytes) and a 1 GiB copy_ (read + write bytes)",
+            "gemm_tflops": {k: round(v, 1) for k, v in mm.items()}}
 
 
 def gemm_compare(dev, M, C, Hm, steps, warmup):
@@ -552,7 +628,10 @@ def config4_section(dev, steps, warmup, model_steps):
     fl = block_flops(B, T, H, W, C, heads, ws)
     with torch.inference_mode():
         ms_blk = timed(lambda: blk(x), steps, warmup)
-    del blk, x
+        y = blk(x)
+    kern, same = block_kernels(blk, x, y, (B, T, H, W, C, heads, ws, shift, torch.bfloat16), "fold2", steps,
+                               warmup)
+    del blk, x, y
     Cc, Hi, Wi, p, depth = 70, 720, 1440, 2, 8
     lat = nsw.misc_utils.era5_latitudes(Hi)
     lon = nsw.misc_utils.era5_longitudes(Wi)
@@ -571,6 +650,7 @@ def config4_section(dev, steps, warmup, model_steps):
     return {"workload": desc + "; model: p2 e512 depth 8, 8 heads, 70 channels on 720x1440, bf16",
             "block_ms": round(ms_blk, 4), "block_tokens_per_s": round(H * W / (ms_blk * 1e-3), 1),
             "block_tflops": round(sum(fl.values()) / (ms_blk * 1e-3) / 1e12, 1),
+            "block_kernels": kern, "ops_path_equals_fused": bool(same),
             "model_ms_per_step": round(ms_model, 3), "model_tflop_per_step": round(step_flops / 1e12, 3),
             "model_tflops": round(step_flops / (ms_model * 1e-3) / 1e12, 1), "finite": ok}
 
@@ -593,13 +673,22 @@ def smooth_fields(shape, sigma, seed, dev):
     return x
 
 
-def model_sections(dev, steps, warmup, with_rollout=True, with_block_calls=True):
-    """Config 3 (one forecast step of the d16 model) and config 5 (8-step
-    rollout, bf16 vs fp32)."""
-    import numpy as np
+# config 3's model: (C_in = C_out, H, W, p, E, depth, heads, window, T)
+C3 = (70, 720, 1440, 4, 1024, 16, 16, (9, 18), 1)
+ROLLOUT_STEPS = 8
+# the fp32 oracle rollout of config3_model + rollout_setup, recorded on the
+# GPU by tests/test_gpu_fullsize.py::test_rollout_config5_bench_setup
+ROLLOUT_GOLDEN = os.path.join(ROOT, "tests", "golden", "rollout_c5_fp32_oracle.json")
+
+
+def config3_model(dev):
+    """The config-3 model (p4, e1024, depth 16, 16 heads, window 9x18, 70
+    channels on 720 x 1440, coordinate positional embedding), random init
+    from seed 3001 (reference trunc-normal(0.02)) held in bf16, and its
+    input field (seed 3002)."""
     import torch
     import nsw
-    C, H, W, p, E, depth, heads, ws, T = 70, 720, 1440, 4, 1024, 16, 16, (9, 18), 1
+    C, H, W, p, E, depth, heads, ws, T = C3
     lat = nsw.misc_utils.era5_latitudes(H)
     lon = nsw.misc_utils.era5_longitudes(W)
     meta = {"coords": nsw.get_spatial_coords((lat, lon)).float(), "sp_shapes": [[H], [W]], "n_channels": C}
@@ -608,6 +697,34 @@ def model_sections(dev, steps, warmup, with_rollout=True, with_block_calls=True)
                                 out_chans=C, embed_dim=E, depth=depth, num_heads=heads, coord_pos_embed=True,
                                 domain_metadata=meta).to(device=dev, dtype=torch.bfloat16).eval()
     x = smooth_fields((1, T, C, H, W), 8.0, 3002, dev)
+    return model, x
+
+
+def rollout_setup(dev):
+    """Config 5's statistics and targets: per-channel mean / std (seed 3003),
+    a climatology near the mean, cos-latitude area weights over the 720 ERA5
+    rows, and ROLLOUT_STEPS normalised target fields (seed 3004)."""
+    import torch
+    import nsw
+    C, H, W = C3[0], C3[1], C3[2]
+    g = torch.Generator().manual_seed(3003)
+    mean = torch.randn(C, generator=g) * 10.0
+    std = torch.rand(C, generator=g) * 1.5 + 0.5
+    clim = mean + std * torch.randn(C, generator=g) * 0.01
+    w = nsw.build_spherical_area_weights(nsw.misc_utils.era5_latitudes(H))[:, None]
+    targets = smooth_fields((ROLLOUT_STEPS, C, H, W), 8.0, 3004, dev)
+    return mean, std, clim, w, targets
+
+
+def model_sections(dev, steps, warmup, with_rollout=True, with_block_calls=True):
+    """Config 3 (one forecast step of the d16 model) and config 5 (8-step
+    rollout, bf16, drift against the fp32 oracle rollout's recorded
+    per-step metrics and against this library's fp32 path)."""
+    import numpy as np
+    import torch
+    import nsw
+    C, H, W, p, E, depth, heads, ws, T = C3
+    model, x = config3_model(dev)
     tokens = (H // p) * (W // p)
     fl = block_flops(1, T, H // p, W // p, E, heads, ws)
     step_flops = depth * sum(fl.values()) + 2 * tokens * (C * p * p) * E * 2   # blocks + embed + head GEMMs
@@ -686,13 +803,8 @@ def model_sections(dev, steps, warmup, with_rollout=True, with_block_calls=True)
         return forecast, None
 
     # config 5: rollout, bf16 and fp32 copies of the same weights
-    S = 8
-    g = torch.Generator().manual_seed(3003)
-    mean = torch.randn(C, generator=g) * 10.0
-    std = torch.rand(C, generator=g) * 1.5 + 0.5
-    clim = mean + std * torch.randn(C, generator=g) * 0.01
-    w = nsw.build_spherical_area_weights(lat)[:, None]
-    targets = smooth_fields((S, C, H, W), 8.0, 3004, dev)
+    S = ROLLOUT_STEPS
+    mean, std, clim, w, targets = rollout_setup(dev)
     res = {}
     for name, dt in (("bf16", torch.bfloat16), ("fp32", torch.float32)):
         m = model if dt == torch.bfloat16 else model.float()
@@ -707,17 +819,31 @@ def model_sections(dev, steps, warmup, with_rollout=True, with_block_calls=True)
         res[name] = (r.cpu().numpy(), a.cpu().numpy(), t0.elapsed_time(t1) / S)
     rb, ab, msb = res["bf16"]
     rf, af, msf = res["fp32"]
+    rnd = lambda a: [round(float(v), 6) for v in a]
     rollout = {
         "workload": "config 5: config-3 model, 8 autoregressive steps from one seeded initial condition, "
                     "per-step latitude-weighted RMSE and ACC over 70 channels (unnormalised fields)",
-        "drift_reference": "the same weights through this library's fp32 path; the drift against the fp32 "
-                           "oracle rollout is checked by tests/test_gpu_fullsize.py::test_rollout_config5",
         "steps": S, "ms_per_step_bf16": round(msb, 3), "ms_per_step_fp32": round(msf, 3),
-        "rmse_mean_bf16": [round(float(v), 6) for v in rb.mean(1)],
-        "rmse_rel_drift_max": [round(float(v), 6) for v in (np.abs(rb - rf) / rf).max(1)],
-        "acc_mean_bf16": [round(float(v), 6) for v in ab.mean(1)],
-        "acc_abs_drift_max": [round(float(v), 6) for v in np.abs(ab - af).max(1)],
+        "rmse_mean_bf16": rnd(rb.mean(1)), "acc_mean_bf16": rnd(ab.mean(1)),
     }
+    golden = None
+    if os.path.exists(ROLLOUT_GOLDEN):
+        with open(ROLLOUT_GOLDEN) as fh:
+            golden = json.load(fh)
+    if golden is not None and golden.get("steps") == S and len(golden.get("rmse", [])) == S:
+        ro_r, ro_a = np.asarray(golden["rmse"]), np.asarray(golden["acc"])
+        rollout["drift_reference"] = ("fp32 oracle rollout (oracle/model_ref.rollout) of the same weights and "
+                                      "inputs, per-step RMSE / ACC recorded in tests/golden/"
+                                      "rollout_c5_fp32_oracle.json")
+        rollout["rmse_rel_drift_max"] = rnd((np.abs(rb - ro_r) / ro_r).max(1))
+        rollout["acc_abs_drift_max"] = rnd(np.abs(ab - ro_a).max(1))
+        rollout["fp32_path_rmse_rel_drift_max"] = rnd((np.abs(rf - ro_r) / ro_r).max(1))
+        rollout["fp32_path_acc_abs_drift_max"] = rnd(np.abs(af - ro_a).max(1))
+    else:
+        rollout["drift_reference"] = "this library's fp32 path (no recorded fp32 oracle rollout found)"
+        rollout["rmse_rel_drift_max"] = rnd((np.abs(rb - rf) / rf).max(1))
+        rollout["acc_abs_drift_max"] = rnd(np.abs(ab - af).max(1))
+    rollout["bf16_vs_fp32_path_rmse_rel_drift_max"] = rnd((np.abs(rb - rf) / rf).max(1))
     return forecast, rollout
 
 

@@ -121,8 +121,9 @@ int nsw_rmsnorm_roll_partition(const void* x, const void* w, float eps, void* xw
 
 /* F.linear + BiasLayer (+ GELU / residual) (models/layer_helpers.py:41-42,71-72,
  * models/mlp.py:80-93): y[M,N] = epi(x[M,K] . w[N,K]^T).  bias / residual may
- * be NULL when the epilogue does not use them.  Requires K % 64 == 0 (bf16) or
- * K % 32 == 0 (f32), N % 8 == 0, 16-byte aligned x, w, y and residual. */
+ * be NULL when the epilogue does not use them.  Requires K % 32 == 0 (bf16) or
+ * K % 16 == 0 (f32) (one MFMA step of k), N % 8 == 0, 16-byte aligned x, w, y
+ * and residual. */
 int nsw_linear(const void* x, const void* w, const void* bias, const void* residual, void* y,
                int64_t M, int64_t N, int64_t K, int epilogue, int dtype, void* stream);
 
@@ -130,7 +131,8 @@ int nsw_linear(const void* x, const void* w, const void* bias, const void* resid
  * (models/swin_helpers.py:216-234): qkv[M, 3C] = x[M,C] . wqkv[3C,C]^T + bqkv,
  * then columns [0,C) (q) and [C,2C) (k) are RMS-normalised per head of hd
  * columns with weights qn_w[hd], kn_w[hd].  wqkv/bqkv are the q, k, v weights
- * / biases stacked in that order.  Requires C % 64 == 0, hd in {16,32,64}. */
+ * / biases stacked in that order.  Requires C % 16 == 0, hd in {4,8,16,32,64}
+ * and C (the GEMM's k) a multiple of 32 (bf16) / 16 (f32). */
 int nsw_qkv_projection(const void* x, const void* wqkv, const void* bqkv, const void* qn_w,
                        const void* kn_w, float eps, void* qkv, int64_t M, int64_t C,
                        int64_t num_heads, int dtype, void* stream);
@@ -191,10 +193,11 @@ typedef struct nsw_block_params {
    * the QKV GEMM.  Both given: the block runs as the one-block window-order
    * chain of nsw_swin_blocks_forward (partition + norm1 sums, QKV with norm1
    * as a row scale, attention, proj + norm2 sums in window order, fc1, fc2
-   * scattering to tokens: 6 launches, the fastest form).  w1_n2 alone: norm1
-   * gather, proj scattering to tokens with the sums (6 launches).  wqkv_n1
-   * alone: the QKV GEMM gathers token rows and sums their squares itself
-   * (slower), norm2 as a pass. */
+   * scattering to tokens: 6 launches).  w1_n2 alone: norm1 gather, proj
+   * scattering to tokens with the sums (6 launches, the default of
+   * nsw.Block; both 6-launch forms measure the same at config 2).  Neither:
+   * norm2 as a pass of its own (7 launches).  wqkv_n1 alone is refused
+   * (NSW_ERR_INVALID). */
   const void* wqkv_n1;   /* [3C, C] or NULL                                     */
   const void* w1_n2;     /* [Hm, C] or NULL                                     */
 } nsw_block_params;
@@ -300,29 +303,6 @@ int nsw_weighted_metrics_unnorm_noalloc(const void* pred, int pred_dtype, const 
                                         int64_t w_cols, const float* clim, int64_t P, int64_t H, int64_t W,
                                         int64_t Cch, double* rmse, double* acc, void* stream);
 
-/* Block.forward's first half with norm1 fused (models/swin_helpers.py:446 +
- * :402-412 + WindowMultiHeadAttention.forward :212-241): qkv[m] (window order,
- * [B*nW*T*wa, 3C]) = per-head-q/k-RMSNorm(rs[t] * (x[t] . wqkv_n^T) + bqkv) with
- * t = token of window row m (roll by -shift + window_partition),
- * rs[t] = 1/sqrt(mean_c x[t,c]^2 + eps) and wqkv_n = wqkv * norm1_w per input
- * column: the same value as nsw_rmsnorm_roll_partition followed by
- * nsw_qkv_projection, in one GEMM whose copies gather the token rows.
- * x [B,T,H,W,C].  Requires C % 64 == 0, hd in {16,32,64}. */
-int nsw_qkv_projection_norm_gather(const void* x, const void* wqkv_n, const void* bqkv,
-                                   const void* qn_w, const void* kn_w, float eps, void* qkv,
-                                   int64_t B, int64_t T, int64_t H, int64_t W, int64_t C,
-                                   int64_t num_heads, int64_t ws0, int64_t ws1, int64_t s0,
-                                   int64_t s1, int dtype, void* stream);
-
-/* y = epi(RMSNorm(x; norm_w, eps) . W^T) (Block.forward's norm2 + MLP fc1,
- * models/swin_helpers.py:457, models/mlp.py:80-85) as one GEMM: w_n[n,k] =
- * W[n,k] * norm_w[k]; the row norms of x are accumulated from the GEMM's own
- * x fragments and applied before the bias.  Epilogues and requirements as
- * nsw_linear. */
-int nsw_linear_rownorm(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
-                       int64_t M, int64_t N, int64_t K, int epilogue, float eps, int dtype,
-                       void* stream);
-
 /* y = epi(RMSNorm(x; norm_w, eps) . W^T) (norm2 + MLP fc1, models/swin_helpers.py
  * :457, models/mlp.py:80-85) with the row statistics supplied by x's producer:
  * w_n[n,k] = W[n,k] * norm_w[k], rs[m] = 1/sqrt(sum_p row_sumsq[m*nparts + p] / K
@@ -340,7 +320,8 @@ int nsw_linear_rowscale(const void* x, const void* w_n, const void* bias, const 
  * (x[m] . wqkv_n^T) + bqkv), wqkv_n = wqkv * norm1_w per input column, rs[m]
  * = 1/sqrt(sum_p row_sumsq[m*nparts + p] / C + eps).  x [M, C] in any row
  * order (window order in the blocks), qkv [M, 3C]; row_sumsq 16-byte
- * aligned.  Requires C % 64 == 0, hd in {16,32,64}. */
+ * aligned.  Requires C % 16 == 0, hd in {4,8,16,32,64} and C (the GEMM's k)
+ * a multiple of 32 (bf16) / 16 (f32). */
 int nsw_qkv_projection_rowscale(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w,
                                 const void* kn_w, float eps, void* qkv, const float* row_sumsq,
                                 int64_t nparts, int64_t M, int64_t C, int64_t num_heads, int dtype,
@@ -396,7 +377,7 @@ int nsw_unpatchify(const void* y, void* out, int64_t B, int64_t C_out, int64_t H
  * out[b*out_bstride + (c*H + i*p + u)*W + j*p + v] in out_dtype (dtype, or
  * float32 for a bf16 GEMM: the bf16-rounded values widened, as nsw_linear +
  * nsw_unpatchify give).  Requires p in {1, 2, 4, 8, 16}, p | H, p | W,
- * K a multiple of 64 (bf16) / 32 (f32), out_bstride >= C_out*H*W and a
+ * K a multiple of 32 (bf16) / 16 (f32), out_bstride >= C_out*H*W and a
  * multiple of p, out aligned to min(16, p * element size) bytes, x and
  * w_perm 16-byte aligned. */
 int nsw_head_unpatchify(const void* x, const void* w_perm, void* out, int64_t B, int64_t C_out, int64_t H,

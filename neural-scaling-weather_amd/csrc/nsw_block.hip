@@ -15,12 +15,7 @@
 //   K6' u   = gelu(rs2 . (h1 . w1_n2^T) + b1),  rs2 = 1/sqrt(sum(S row) / C + eps)
 //
 // (6 launches, the default of nsw.Block).  With wqkv_n1 = Wqkv * norm1 as
-// well, K1 folds into the QKV GEMM, which gathers the token rows and
-// accumulates their sums of squares from its own fragments:
-//
-//   K2' qkv = per-head-norm(rs1 . (gather(x) . wqkv_n1^T) + b)
-//
-// (5 launches; measured slower than K1 + K2 on MI355X, kept as an option).
+// well, the block runs as a one-block window-order chain (below).
 //
 // Workspace: A [M*C] holds xw, then o, then hn; Q [M*max(3C, Hm)] holds qkv,
 // then u; H1 [M*C] holds h1 (dtype elements); S [M*nparts] float.
@@ -37,11 +32,6 @@ int gemm_linear_rowscale(const void* x, const void* w_n, const void* bias, const
                          const float* row_sumsq, int64_t nparts, int64_t M, int64_t N, int64_t K, int epilogue,
                          float eps, int dtype, void* stream);
 int64_t sumsq_parts(int64_t C, int dtype);
-int gemm_qkv_norm_gather(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w,
-                         const void* kn_w, float eps, void* qkv, int64_t B, int64_t T, int64_t H, int64_t W,
-                         int64_t C, int64_t num_heads, int64_t ws0, int64_t ws1, int64_t s0, int64_t s1,
-                         int dtype, void* stream);
-
 int gemm_qkv_rowscale(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w, const void* kn_w,
                       float eps, void* qkv, const float* row_sumsq, int64_t nparts, int64_t M, int64_t C,
                       int64_t num_heads, int dtype, void* stream);
@@ -114,20 +104,15 @@ extern "C" int nsw_swin_block_forward(const void* x, void* y, const nsw_block_pa
     // window order, fc2 scatters to tokens)
     return nsw_swin_blocks_forward(x, y, p, s, 1, workspace, workspace_bytes, stream);
   }
-  if (p->wqkv_n1) {
-    // K2'
-    rc = gemm_qkv_norm_gather(x, p->wqkv_n1, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, s->B, s->T, s->H, s->W, C,
-                              s->num_heads, s->ws0, s->ws1, s->s0, s->s1, s->dtype, stream);
-    if (rc) return rc;
-  } else {
-    // K1
-    rc = nsw_rmsnorm_roll_partition(x, p->norm1_w, s->eps, A, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1,
-                                    s->s0, s->s1, s->dtype, stream);
-    if (rc) return rc;
-    // K2
-    rc = gemm_qkv(A, p->wqkv, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, M, C, s->num_heads, s->dtype, stream);
-    if (rc) return rc;
-  }
+  NSW_CHECK_ARG(!p->wqkv_n1, "%s: wqkv_n1 (norm1 folded) needs w1_n2 as well (the one-block window-order chain)",
+                what);
+  // K1
+  rc = nsw_rmsnorm_roll_partition(x, p->norm1_w, s->eps, A, s->B, s->T, s->H, s->W, C, s->ws0, s->ws1, s->s0,
+                                  s->s1, s->dtype, stream);
+  if (rc) return rc;
+  // K2
+  rc = gemm_qkv(A, p->wqkv, p->bqkv, p->qn_w, p->kn_w, s->eps, Q, M, C, s->num_heads, s->dtype, stream);
+  if (rc) return rc;
   // K3 (o overwrites xw in A)
   rc = nsw_window_attention(Q, A, nullptr, 0, M / L, L, C, s->num_heads, 1.0f / sqrtf((float)hd), s->H,
                             s->W, s->ws0, s->ws1, s->s0, s->s1, s->T, s->dtype, stream);

@@ -102,28 +102,6 @@ __device__ __forceinline__ void mfma_chunk(f32x4& acc, const u32x4& a, const u32
   }
 }
 
-// Sum of squares of the 8 bf16 (4 f32) values of one 16-byte fragment, added to s.
-// bf16: v_dot2c_f32_bf16 (s += lo*lo + hi*hi) per dword, issued through inline
-// asm: with the builtin (ROCm 7.2 clang) the four dword extracts of the
-// fragment were folded into the first one (every dot2 read dword 0).
-template <typename T>
-__device__ __forceinline__ float frag_sumsq(const u32x4& f, float s) {
-  if constexpr (sizeof(T) == 2) {
-    const uint32_t d0 = f[0], d1 = f[1], d2 = f[2], d3 = f[3];
-    asm("v_dot2c_f32_bf16 %0, %1, %1" : "+v"(s) : "v"(d0));
-    asm("v_dot2c_f32_bf16 %0, %1, %1" : "+v"(s) : "v"(d1));
-    asm("v_dot2c_f32_bf16 %0, %1, %1" : "+v"(s) : "v"(d2));
-    asm("v_dot2c_f32_bf16 %0, %1, %1" : "+v"(s) : "v"(d3));
-  } else {
-    const f32x4 v = __builtin_bit_cast(f32x4, f);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s = fmaf(v[i], v[i], s);
-  }
-  return s;
-}
-
-
-
 // Fragment read: 16 bytes of k chunk `chunk` of a stage row.
 __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk) {
   const int slot = chunk ^ row_swizzle(row);
@@ -146,7 +124,7 @@ __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk)
 template <typename T, int PRE>
 __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X, const T* __restrict__ Wt, int M,
                                              int N, int K, int m0, int n0, const EpiArgs& ea,
-                                             f32x4 (&acc)[NB][MB], float (&ssr)[MB], int wave, int lane) {
+                                             f32x4 (&acc)[NB][MB], int wave, int lane) {
   constexpr int SLOT = 256 * ROWB;        // one operand's stage: 32 KB
   constexpr int NC = SLOT / (NW * 1024);  // copies per wave per operand and stage (4)
   constexpr int WR = 256 / NW;            // stage rows copied by one wave (32)
@@ -164,7 +142,6 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
     const int chunk = (lane % 8) ^ row_swizzle(srow);
     int gx = m0 + srow;
     gx = gx < M ? gx : M - 1;   // rows past the edge re-read the last row (never stored)
-    if constexpr (PRE == PRE_ROWNORM_GATHER) gx = (int)ea.geom.token_of_row(gx);
     int gw = n0 + srow;
     gw = gw < N ? gw : N - 1;
     vx[j] = (uint32_t)gx * rowbytes + chunk * 16;
@@ -180,7 +157,10 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
 #define NSW_COPY_W(sl, st, j) dma16(rw, cbase + NSW_WSLOT(sl) + (j) * 1024, vw[j], (st) * ROWB)
 
   const int nk = K / (STEPB / (int)sizeof(T));   // MFMA steps
-  const int nst = nk / 2;                          // stages
+  // stages; with an odd step count the last stage holds one step's k (its
+  // second half is copied -- the next row's first bytes, or zeros past the
+  // end of the operand -- and never read by an MFMA)
+  const int nst = (nk + 1) / 2;
   // prologue: x0 w0 x1 w1, then wait for x0 and w0 (step 0 issues x2)
 #pragma unroll
   for (int j = 0; j < NC; ++j) NSW_COPY_X(0, 0, j);
@@ -248,12 +228,6 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
         _Pragma("unroll") for (int mb = 0; mb < MB; ++mb)                                      \
           mfma_chunk<T>(acc[nb][mb], fa[(U) & 1][nb], fb[(U) & 1][mb]);                        \
         fa[((U) + 1) & 1][nb] = lds_frag(smem + NSW_WSLOT(nsu_), wrow + nb * 16, nsub_ * 4 + fg); \
-        if constexpr (pre_sums_in_loop(PRE)) {                                                 \
-          _Pragma("unroll") for (int q = 0; q < MB / NB; ++q) {                                \
-            const int mq = nb * (MB / NB) + q;                                                 \
-            ssr[mq] = frag_sumsq<T>(fb[(U) & 1][mq], ssr[mq]);                                 \
-          }                                                                                    \
-        }                                                                                      \
         /* the group's three fragment reads spread over its MFMAs: 1, 2 MFMAs, 1, */            \
         /* 3 MFMAs, 1, 3 MFMAs (bf16; four MFMA instructions per block in fp32)   */            \
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                                     \
@@ -372,12 +346,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   for (int i = 0; i < NB; ++i)
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float ssr[MB];                                  // PRE: this lane's part of the row sums of squares
-#pragma unroll
-  for (int i = 0; i < MB; ++i) ssr[i] = 0.f;
   const int frow = lane & 15, fg = lane >> 4;
 
-  mainloop_256<T, PRE>(smem, X, Wt, M, N, K, m0, n0, ea, acc, ssr, wave, lane);
+  mainloop_256<T, PRE>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane);
 
   // ---------------------------------------------------------------- epilogue
   // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
@@ -451,13 +422,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
     p_rs = 1.0f / sqrtf(ss / (float)K + ea.eps);
   }
 
-  // PRE: the four lane groups hold the four k chunks of each x row
+  // PRE_ROWSCALE: the row scales of this lane's rows (from LDS, below)
   float rsr[MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    rsr[mb] = 1.f;
-    if constexpr (pre_sums_in_loop(PRE)) rsr[mb] = 1.0f / sqrtf(rows4_sum(ssr[mb]) / (float)K + ea.eps);
-  }
+  for (int mb = 0; mb < MB; ++mb) rsr[mb] = 1.f;
   // 1. epilogue math of row block mb in the fragment layout (bias, row scale,
   // head norm, GELU), evaluated where the block is staged
   auto row_values = [&](int mb, float (&v)[NB][4]) {
@@ -726,7 +694,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
 template <typename T, int EPI, int PRE = PRE_NONE>
 static int launch_gemm(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K,
                        const EpiArgs& ea, hipStream_t st, const char* what) {
-  constexpr int KT = 128 / sizeof(T);
+  constexpr int KT = STEPB / sizeof(T);   // one MFMA step of k: 32 (bf16) / 16 (f32)
   NSW_CHECK_ARG(M > 0 && N > 0 && K > 0, "%s: M, N, K must be positive", what);
   NSW_CHECK_ARG(K % KT == 0, "%s: K=%lld must be a multiple of %d", what, (long long)K, KT);
   NSW_CHECK_ARG(N % 8 == 0, "%s: N=%lld must be a multiple of 8", what, (long long)N);
@@ -833,38 +801,6 @@ int gemm_linear_rowscale(const void* x, const void* w_n, const void* bias, const
   }
 }
 
-// QKV projection of RMSNorm(x) gathered into window order: qkv[m] =
-// headnorm(rs[t] * (x[t] . wqkv_n^T) + bqkv), t = token_of_row(m),
-// wqkv_n = wqkv * norm1_w (per input column, prepared by the caller).
-int gemm_qkv_norm_gather(const void* x, const void* wqkv_n, const void* bqkv, const void* qn_w,
-                         const void* kn_w, float eps, void* qkv, int64_t B, int64_t T, int64_t H, int64_t W,
-                         int64_t C, int64_t num_heads, int64_t ws0, int64_t ws1, int64_t s0, int64_t s1,
-                         int dtype, void* stream) {
-  const char* what = "nsw_qkv_projection_norm_gather";
-  int rc = check_geom(B, T, H, W, ws0, ws1, what);
-  if (rc) return rc;
-  NSW_CHECK_ARG(num_heads > 0 && C % num_heads == 0, "%s: C=%lld not divisible by num_heads=%lld", what,
-                (long long)C, (long long)num_heads);
-  const int64_t hd = C / num_heads;
-  NSW_CHECK_ARG(C % 16 == 0, "%s: C=%lld must be a multiple of 16", what, (long long)C);
-  NSW_CHECK_ARG(hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64,
-                "%s: head_dim=%lld unsupported (4, 8, 16, 32, 64)", what, (long long)hd);
-  NSW_CHECK_ARG(bqkv && qn_w && kn_w, "%s: bias and norm weights are required", what);
-  NSW_CHECK_ARG(x != (const void*)qkv, "%s: x and qkv must not alias", what);
-  EpiArgs ea{};
-  ea.bias = bqkv; ea.qn_w = qn_w; ea.kn_w = kn_w; ea.eps = eps; ea.C = (int)C;
-  ea.group_m = 4;
-  ea.geom = WinGeom::make((int)B, (int)T, (int)H, (int)W, (int)ws0, (int)ws1, (int)(s0 % H), (int)(s1 % W));
-  const int64_t M = B * T * H * W;
-  if (hd == 64)
-    return dispatch_gemm<EPI_QKV_HN64, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
-  if (hd == 32)
-    return dispatch_gemm<EPI_QKV_HN32, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
-  if (hd == 8) return dispatch_gemm<EPI_QKV_HN8, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
-  if (hd == 4) return dispatch_gemm<EPI_QKV_HN4, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
-  return dispatch_gemm<EPI_QKV_HN16, PRE_ROWNORM_GATHER>(dtype, x, wqkv_n, qkv, M, 3 * C, C, ea, stream, what);
-}
-
 // QKV projection of rows whose RMSNorm (norm1) comes as a row scale from the
 // producer's partial sums of squares: qkv[m] = headnorm(rs1[m] * (x[m] .
 // wqkv_n^T) + b), wqkv_n = wqkv * norm1_w per input column, rs1 =
@@ -933,43 +869,9 @@ int gemm_linear_remap(const void* x, const void* w, const void* bias, const void
   return dispatch_gemm<EPI_REMAP_RESIDUAL>(dtype, x, w, y, M, N, K, ea, stream, what);
 }
 
-// y = epi(RMSNorm(x) . W^T) with w_n = W * norm_w: the row norm of x fused.
-int gemm_linear_rownorm(const void* x, const void* w_n, const void* bias, const void* residual, void* y,
-                        int64_t M, int64_t N, int64_t K, int epilogue, float eps, int dtype, void* stream) {
-  const char* what = "nsw_linear_rownorm";
-  EpiArgs ea{};
-  ea.bias = bias; ea.residual = residual; ea.eps = eps;
-  if (epilogue != NSW_EPI_NONE) NSW_CHECK_ARG(bias != nullptr, "%s: epilogue %d needs a bias", what, epilogue);
-  switch (epilogue) {
-    case NSW_EPI_NONE: return dispatch_gemm<EPI_NONE, PRE_ROWNORM>(dtype, x, w_n, y, M, N, K, ea, stream, what);
-    case NSW_EPI_BIAS: return dispatch_gemm<EPI_BIAS, PRE_ROWNORM>(dtype, x, w_n, y, M, N, K, ea, stream, what);
-    case NSW_EPI_BIAS_GELU:
-      return dispatch_gemm<EPI_BIAS_GELU, PRE_ROWNORM>(dtype, x, w_n, y, M, N, K, ea, stream, what);
-    case NSW_EPI_BIAS_RESIDUAL:
-      NSW_CHECK_ARG(residual != nullptr, "%s: residual epilogue needs a residual", what);
-      return dispatch_gemm<EPI_BIAS_RESIDUAL, PRE_ROWNORM>(dtype, x, w_n, y, M, N, K, ea, stream, what);
-    default: return set_error(NSW_ERR_INVALID, "%s: unknown epilogue %d", what, epilogue);
-  }
-}
-
 }  // namespace nsw
 
 using namespace nsw;
-
-extern "C" int nsw_qkv_projection_norm_gather(const void* x, const void* wqkv_n, const void* bqkv,
-                                              const void* qn_w, const void* kn_w, float eps, void* qkv,
-                                              int64_t B, int64_t T, int64_t H, int64_t W, int64_t C,
-                                              int64_t num_heads, int64_t ws0, int64_t ws1, int64_t s0,
-                                              int64_t s1, int dtype, void* stream) {
-  return gemm_qkv_norm_gather(x, wqkv_n, bqkv, qn_w, kn_w, eps, qkv, B, T, H, W, C, num_heads, ws0, ws1, s0, s1,
-                              dtype, stream);
-}
-
-extern "C" int nsw_linear_rownorm(const void* x, const void* w_n, const void* bias, const void* residual,
-                                  void* y, int64_t M, int64_t N, int64_t K, int epilogue, float eps, int dtype,
-                                  void* stream) {
-  return gemm_linear_rownorm(x, w_n, bias, residual, y, M, N, K, epilogue, eps, dtype, stream);
-}
 
 extern "C" int nsw_linear(const void* x, const void* w, const void* bias, const void* residual, void* y,
                           int64_t M, int64_t N, int64_t K, int epilogue, int dtype, void* stream) {

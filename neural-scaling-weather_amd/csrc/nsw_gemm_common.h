@@ -27,23 +27,15 @@ enum Epi {
   EPI_QKV_HN8 = 72           // one 16-column block (4 / 8 of its columns)
 };
 
-// Operand-side fusions (template parameter PRE):
+// Operand-side fusion (template parameter PRE):
 //   PRE_NONE     y = epi(x . w^T)
-//   PRE_ROWNORM  y = epi(rs . (x . w^T)) with rs[m] = 1/sqrt(mean_k x[m,k]^2 + eps):
-//                the RMSNorm of the rows of x with its weight folded into w
-//                (w[n,k] = W[n,k] * norm_w[k], prepared by the caller), so
-//                that x . w^T * rs = RMSNorm(x) . W^T.  The sums of squares
-//                are accumulated from the x fragments the MFMAs consume
-//                (v_dot2c_f32_bf16 / FMA), rs is applied before the bias.
-//   PRE_ROWNORM_GATHER  as PRE_ROWNORM, and the copy of x row m reads token
-//                row token_of_row(m) of the image (roll by -shift + window
-//                partition folded into the copy addresses).
 //   PRE_ROWSCALE y = epi(rs . (x . w^T)) with rs[m] = 1/sqrt(sum_p P[m,p] / K + eps)
 //                from per-row partial sums of squares P [M, nparts] written by
-//                the producer of x (the proj scatter epilogue): the norm costs
-//                the consumer one read per row instead of a pass over x.
-enum Pre { PRE_NONE = 0, PRE_ROWNORM = 1, PRE_ROWNORM_GATHER = 2, PRE_ROWSCALE = 3 };
-constexpr bool pre_sums_in_loop(int pre) { return pre == PRE_ROWNORM || pre == PRE_ROWNORM_GATHER; }
+//                the producer of x (the proj scatter / remap epilogues): the
+//                RMSNorm of the rows of x with its weight folded into w
+//                (w[n,k] = W[n,k] * norm_w[k], prepared by the caller), at
+//                one read per row instead of a pass over x.
+enum Pre { PRE_NONE = 0, PRE_ROWSCALE = 3 };
 
 constexpr int qkv_head_dim(int epi) {
   return (epi == EPI_QKV_HN16 || epi == EPI_QKV_HN32 || epi == EPI_QKV_HN64) ? epi

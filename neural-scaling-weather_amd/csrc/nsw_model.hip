@@ -388,8 +388,10 @@ extern "C" int nsw_patch_im2col(const void* x, const void* inv, int64_t B, int64
   NSW_CHECK_ARG(B * T * C_x * H * W < (1LL << 40) && H * W < (1LL << 31), "%s: too large", what);
   const int64_t M = B * T * (H / p) * (W / p);
   const size_t es = dtype_size(out_dtype);
-  // float images with p = 2 or 4: the direct-to-LDS kernel
-  if (x_dtype == NSW_DTYPE_F32 && (p == 2 || p == 4) && W % 4 == 0 && ((uintptr_t)x % 16) == 0 &&
+  // float images with p = 2 or 4: the direct-to-LDS kernel (its buffer
+  // ranges and byte offsets into one image plane are 32-bit: H*W*4 < 2^31)
+  if (x_dtype == NSW_DTYPE_F32 && (p == 2 || p == 4) && W % 4 == 0 && H * W * 4 < (1LL << 31) &&
+      ((uintptr_t)x % 16) == 0 &&
       (inv == nullptr || ((uintptr_t)inv % 16) == 0)) {
     constexpr int NB = IM2COL_DMA_NB;
     const int CG = NB / (int)p, TG = 256 / (int)p;

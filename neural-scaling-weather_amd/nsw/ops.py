@@ -230,47 +230,6 @@ def qkv_projection(x: torch.Tensor, wqkv: torch.Tensor, bqkv: torch.Tensor, qn_w
 
 # --------------------------------------------------------------- attention ---
 
-def qkv_projection_norm_gather(x: torch.Tensor, wqkv_n: torch.Tensor, bqkv: torch.Tensor, qn_w: torch.Tensor,
-                               kn_w: torch.Tensor, num_heads: int, window_size, shift_size,
-                               eps: Optional[float] = None) -> torch.Tensor:
-    """x [B,T,H,W,C] (token order) -> qkv [B*nW, T*wa, 3C] (window order):
-    RMSNorm (weight folded into wqkv_n), roll + partition and the QKV
-    projection with per-head q/k RMSNorm in one GEMM."""
-    dev = _dev(x, wqkv_n, bqkv, qn_w, kn_w)
-    _same_dtype(x, wqkv_n, bqkv, qn_w, kn_w)
-    B, T, H, W, C = x.shape
-    eps = default_eps(x.dtype) if eps is None else float(eps)
-    ws0, ws1 = window_size
-    y = torch.empty(B * (H // ws0) * (W // ws1), T * ws0 * ws1, 3 * C, dtype=x.dtype, device=dev)
-    check(lib().nsw_qkv_projection_norm_gather(x.data_ptr(), wqkv_n.data_ptr(), bqkv.data_ptr(), qn_w.data_ptr(),
-                                               kn_w.data_ptr(), eps, y.data_ptr(), B, T, H, W, C, num_heads,
-                                               window_size[0], window_size[1], shift_size[0], shift_size[1],
-                                               dtype_code(x), _stream(dev)), "qkv_projection_norm_gather")
-    return y
-
-
-def linear_rownorm(x: torch.Tensor, w_n: torch.Tensor, bias: Optional[torch.Tensor] = None,
-                   residual: Optional[torch.Tensor] = None, epilogue: Optional[int] = None,
-                   eps: Optional[float] = None) -> torch.Tensor:
-    """y = epi(RMSNorm(x) . W^T) with w_n = W * norm_w (the norm weight
-    folded in), the row norms of x computed inside the GEMM."""
-    dev = _dev(x, w_n, bias, residual)
-    _same_dtype(x, w_n, bias, residual)
-    K = x.shape[-1]
-    N, Kw = w_n.shape
-    if Kw != K:
-        raise ValueError(f"linear_rownorm: x has {K} features, weight expects {Kw}")
-    M = x.numel() // K
-    if epilogue is None:
-        epilogue = _lib.NSW_EPI_NONE if bias is None else (
-            _lib.NSW_EPI_BIAS if residual is None else _lib.NSW_EPI_BIAS_RESIDUAL)
-    eps = default_eps(x.dtype) if eps is None else float(eps)
-    y = torch.empty(x.shape[:-1] + (N,), dtype=x.dtype, device=dev)
-    check(lib().nsw_linear_rownorm(x.data_ptr(), w_n.data_ptr(), _p(bias), _p(residual), y.data_ptr(), M, N, K,
-                                   int(epilogue), eps, dtype_code(x), _stream(dev)), "linear_rownorm")
-    return y
-
-
 def window_attention(qkv: torch.Tensor, num_heads: int, scale: float, mask: Optional[torch.Tensor] = None,
                      geometry: Optional[Tuple[int, int, Tuple[int, int], Tuple[int, int], int]] = None
                      ) -> torch.Tensor:
@@ -416,19 +375,29 @@ def linear_remap_residual(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor, 
 # ------------------------------------------------------------------- block ---
 
 _ws_lock = threading.Lock()
-_workspaces = {}
+_workspaces = {}      # (device index, stream) -> [buffer, handed out under graph capture]
+_ws_retired = []      # replaced buffers that a captured graph may still address
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     """Grow-only scratch buffer per (device, stream), reused by every block
-    launched on that stream (kernels on one stream run in order)."""
+    launched on that stream (kernels on one stream run in order).  A buffer
+    handed out while the stream was being captured into a CUDA graph is
+    never freed: when a later, larger call replaces it, it moves to a list
+    kept for the life of the process, so that replays of the graph keep
+    writing memory they own."""
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    capturing = torch.cuda.is_current_stream_capturing()
     with _ws_lock:
-        buf = _workspaces.get(key)
-        if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
-            _workspaces[key] = buf
-        return buf
+        ent = _workspaces.get(key)
+        if ent is None or ent[0].numel() < nbytes:
+            if ent is not None and ent[1]:
+                _ws_retired.append(ent[0])
+            ent = [torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device), False]
+            _workspaces[key] = ent
+        if capturing:
+            ent[1] = True
+        return ent[0]
 
 
 def block_shape(x: torch.Tensor, num_heads: int, window_size, shift_size, hidden: int,
@@ -561,7 +530,9 @@ def weighted_metrics(pred: torch.Tensor, target: torch.Tensor, weights: torch.Te
 # ------------------------------------------------------------ model layout ---
 
 def k_granule(dtype: torch.dtype) -> int:
-    """GEMM k granularity of nsw_linear: 64 (bf16) / 32 (f32) elements."""
+    """K padding of the patch matrix: one 128-byte operand stage of the GEMM,
+    64 (bf16) / 32 (f32) elements, so that its rows start on whole cache
+    lines (the GEMM itself takes K a multiple of 32 / 16)."""
     return 64 if dtype == torch.bfloat16 else 32
 
 

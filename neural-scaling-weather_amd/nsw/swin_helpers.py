@@ -190,9 +190,8 @@ class Block(nn.Module):
         # block runs as a one-block window-order chain -- a partition pass
         # that also writes the norm1 row sums, the QKV GEMM with norm1 as a
         # row scale, h1 kept in window order, fc2 scattering to tokens (6
-        # launches, the same time at config 2).  fold_norm1 alone: the QKV
-        # GEMM gathers the token rows and sums their squares in its main
-        # loop (slower).
+        # launches, the same time at config 2).  fold_norm1 implies
+        # fold_norm2 (the chain needs both folded weights).
         self.fold_norm1 = False
         self.fold_norm2 = True
 
@@ -211,7 +210,8 @@ class Block(nn.Module):
         weights are included as fold_norm1 / fold_norm2 ask, or both when
         ``fold_all`` (the window-order chain of SwinTransformer.forward)."""
         a = self.attn
-        fold1, fold2 = self.fold_norm1 or fold_all, self.fold_norm2 or fold_all
+        fold1 = self.fold_norm1 or fold_all
+        fold2 = self.fold_norm2 or fold1
         if torch.compiler.is_compiling():
             # traced: built from the parameters each call (the cache key reads data_ptr)
             return self._build_pack(fold1, fold2)
@@ -275,7 +275,7 @@ class Block(nn.Module):
         """x [B, T, H, W, C] -> [B, T, H, W, C] (models/swin_helpers.py:435-459)."""
         self.check_input(x)
         pk = self.packed()
-        drop = ([] if self.fold_norm1 else ["wqkv_n1"]) + ([] if self.fold_norm2 else ["w1_n2"])
+        drop = ([] if self.fold_norm1 else ["wqkv_n1"]) + ([] if self.fold_norm2 or self.fold_norm1 else ["w1_n2"])
         if drop:
             pk = {k: v for k, v in pk.items() if k not in drop}
         return torch.ops.nsw.swin_block(x, torch_ops.block_param_list(pk), self.num_heads,

@@ -82,6 +82,35 @@ def test_chain_fp32(device, B, T, H, W, C, heads, ws, shifts):
     assert rel_l2(y, y_sep) < 2e-6
 
 
+def test_chain_fp32_production_width(device):
+    """fp32 (the reference's inference precision) at config 2's geometry and
+    width: 180x360 tokens, C=1024, 16 heads (hd 64), window 9x18, four
+    blocks with alternating shift.  The chain of the first d + 1 blocks is
+    checked against the oracle block d applied to the chain's own output
+    after d blocks (every block within 1e-5, north_star's fp32 bar), and the
+    whole stack against the oracle stack; oracle in fp32 on the device."""
+    T, H, W, C, heads, ws = 1, 180, 360, 1024, 16, (9, 18)
+    shifts = ALT * 2
+    eps = torch.finfo(torch.float32).eps
+    blocks, params = make_stack(device, torch.float32, T, H, W, C, heads, ws, shifts, seed=6)
+    x = synth.activations((1, T, H, W, C), seed=66).to(device)
+    errs = []
+    with torch.inference_mode():
+        prev = x
+        for d in range(len(shifts)):
+            y = run_chain(blocks[:d + 1], x)
+            pd = {k: v.to(device) for k, v in params[d].items()}
+            want = ref.block_forward(prev, pd, heads, ws, shifts[d], eps=eps)
+            errs.append(rel_l2(y, want))
+            prev = y
+        want_all = oracle_stack(x, params, heads, ws, shifts, eps, device=device)
+        e_all = rel_l2(prev, want_all)
+    torch.cuda.synchronize()
+    print(f"fp32 chain at C=1024: per block {[f'{e:.2e}' for e in errs]}, stack {e_all:.2e}", flush=True)
+    assert max(errs) < 1e-5
+    assert e_all < 1e-5 * len(shifts)
+
+
 def test_chain_bf16_config2(device):
     """Four blocks at config 2's geometry (180x360, C=1024, 16 heads, window
     9x18, alternating shift), bf16; oracle in fp32 on the device."""

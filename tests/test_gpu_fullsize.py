@@ -126,6 +126,30 @@ def test_model_fullsize_bf16(device, name):
     torch.cuda.empty_cache()
 
 
+def test_model_config3_fp32(device):
+    """Config 3's model (p4, e1024, depth 16, 16 heads, 70 channels,
+    720x1440) in fp32, the reference's inference precision
+    (utils/inferencer.py:337-449 runs without autocast): the forward (patch
+    embedding into block 0's window order, the window-order block chain,
+    the fused head) against the fp32 oracle model on the device, within
+    1e-5 relative L2 per stage (embedding, 16 blocks, head)."""
+    C, H, W, p, E, heads, ws, depth = CONFIGS["config3"]
+    print(f"config3 fp32: p{p} e{E} d{depth} {C}x{H}x{W}", flush=True)
+    model, prm, coords = build(device, "config3", seed=11)
+    model = model.float()                               # the bf16-rounded weights, in fp32
+    x = synth.smooth_field((1, 1, C, H, W), 8.0, 3002).to(device)
+    with torch.inference_mode():
+        got = model(x)
+        assert got.dtype == torch.float32 and model.chain_blocks
+        want = mr.model_forward(x, prm, patch_size=p, window_size=ws, depth=depth, num_heads=heads,
+                                out_chans=C, coords=coords)
+        e2e = rel_l2(got, want)
+    print(f"  end-to-end after {depth} blocks: {e2e:.3e}", flush=True)
+    assert e2e < 1e-5 * (depth + 2)
+    del model, prm, got, want
+    torch.cuda.empty_cache()
+
+
 def test_rollout_config5(device):
     """Config 5: 8 autoregressive steps of the config-3 model (bf16, nsw.Rollout
     with the fused unnormalising RMSE/ACC) against the oracle rollout of the
@@ -171,3 +195,60 @@ def test_rollout_config5(device):
     assert adrift.max() < 1e-2
     del model, prm, f0, f1
     torch.cuda.empty_cache()
+
+
+def test_rollout_config5_bench_setup(device):
+    """Config 5 on bench.py's own model and inputs (bench.config3_model,
+    bench.rollout_setup): the bf16 rollout (nsw.Rollout) against the fp32
+    oracle rollout of the same weights (bf16 values in fp32) and inputs.
+    The oracle's per-step RMSE / ACC are what bench.py's rollout drift is
+    measured against: they are kept in tests/golden/rollout_c5_fp32_oracle.json
+    (written to $NSW_GOLDEN_OUT when set) and must be reproduced here."""
+    import os
+    import sys
+    import nsw
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    if root not in sys.path:
+        sys.path.insert(0, root)
+    import bench
+    C, H, W, p, E, depth, heads, ws, T = bench.C3
+    S = bench.ROLLOUT_STEPS
+    model, x = bench.config3_model(device)
+    mean, std, clim, w, targets = bench.rollout_setup(device)
+    print(f"config5 (bench setup): {S} steps, bf16 vs the fp32 oracle", flush=True)
+    with torch.inference_mode():
+        r1, a1, _ = nsw.Rollout(model, mean, std, w, clim=clim).run(x, targets)
+        torch.cuda.synchronize()
+        prm = {k: v.float() for k, v in model.state_dict().items()}
+        coords = model.coords.float()
+
+        def oracle_model(inp):
+            return mr.model_forward(inp, prm, patch_size=p, window_size=ws, depth=depth, num_heads=heads,
+                                    out_chans=C, coords=coords)
+
+        r0, a0, _ = mr.rollout(oracle_model, x, None, targets, mean, std, w[:, 0].double().numpy(), clim)
+    r1, a1, r0, a0 = r1.cpu().numpy(), a1.cpu().numpy(), r0.numpy(), a0.numpy()
+    rdrift = (np.abs(r1 - r0) / r0).max(axis=1)
+    adrift = np.abs(a1 - a0).max(axis=1)
+    rec = {"steps": S, "channels": C,
+           "setup": "bench.config3_model (seeds 3001 / 3002) + bench.rollout_setup (seeds 3003 / 3004); "
+                    "oracle/model_ref.rollout in fp32 on the GPU, TF32 off",
+           "rmse": [[float(v) for v in row] for row in r0], "acc": [[float(v) for v in row] for row in a0]}
+    out = os.environ.get("NSW_GOLDEN_OUT")
+    if out:
+        with open(out, "w") as fh:
+            json.dump(rec, fh)
+    print(json.dumps({"config5_bench_setup_drift_vs_fp32_oracle": {
+        "rmse_rel_drift_max": [round(float(v), 6) for v in rdrift],
+        "acc_abs_drift_max": [round(float(v), 6) for v in adrift]}}), flush=True)
+    assert rdrift.max() < 1e-2
+    assert adrift.max() < 1e-2
+    golden = os.path.join(root, "tests", "golden", "rollout_c5_fp32_oracle.json")
+    if os.path.exists(golden):
+        with open(golden) as fh:
+            g = json.load(fh)
+        np.testing.assert_allclose(r0, np.asarray(g["rmse"]), rtol=1e-4)
+        np.testing.assert_allclose(a0, np.asarray(g["acc"]), rtol=0, atol=1e-5)
+    del model
+    torch.cuda.empty_cache()
+

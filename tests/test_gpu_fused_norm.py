@@ -1,11 +1,8 @@
-"""GPU parity of the GEMMs with a fused input RMSNorm: the QKV projection
-that gathers token rows into window order and normalises them
-(nsw_qkv_projection_norm_gather), the linear layer with a row norm
-(nsw_linear_rownorm), the proj scatter that also writes its rows' partial
-sums of squares (nsw_proj_reverse_residual_sumsq) and the linear layer that
-takes them (nsw_linear_rowscale), against the fp32 oracle (RMSNorm -> roll
--> partition -> projection, models/swin_helpers.py:446 + :402-412 +
-:212-241; RMSNorm -> fc1, :457 + models/mlp.py:80-85).  Tolerances: fp32
+"""GPU parity of the GEMMs with a fused input RMSNorm: the proj scatter that
+also writes its rows' partial sums of squares
+(nsw_proj_reverse_residual_sumsq) and the linear layer that takes them
+(nsw_linear_rowscale), against the fp32 oracle (RMSNorm -> fc1,
+models/swin_helpers.py:457 + models/mlp.py:80-85).  Tolerances: fp32
 1e-5, bf16 1e-2 relative L2, as for the unfused kernels."""
 import pytest
 import torch
@@ -35,71 +32,6 @@ CASES = [
     (2, 2, 18, 36, 128, 2, (9, 18), (4, 9)),
     (1, 1, 16, 32, 64, 2, (4, 8), (2, 4)),
 ]
-
-
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B,T,H,W,C,heads,ws,shift", CASES)
-def test_qkv_projection_norm_gather(device, dtype, B, T, H, W, C, heads, ws, shift):
-    from nsw import ops
-    M = B * T * H * W
-    if dtype == torch.float32 and M * C * C * 3 > 3e11:
-        pytest.skip("fp32 CPU oracle too slow at this size")
-    hd = C // heads
-    g = torch.Generator().manual_seed(C + H)
-    x = (3.0 * torch.randn(B, T, H, W, C, generator=g) + 0.5).to(dtype)    # rows far from unit RMS
-    n1 = (1 + 0.2 * torch.randn(C, generator=g)).to(dtype)
-    w = synth.trunc_normal((3 * C, C), 0.02, g).to(dtype)
-    b = (0.1 * torch.randn(3 * C, generator=g)).to(dtype)
-    qn = (1 + 0.2 * torch.randn(hd, generator=g)).to(dtype)
-    kn = (1 + 0.2 * torch.randn(hd, generator=g)).to(dtype)
-    eps = torch.finfo(dtype).eps
-    d = lambda t: t.to(device)
-    got = ops.qkv_projection_norm_gather(d(x), d(fold(w, n1, dtype)), d(b), d(qn), d(kn), heads, ws, shift, eps)
-    # oracle
-    xn = ref.rms_norm(x.float(), n1.float(), eps)
-    xw = ref.window_partition(ref.roll(xn, (-shift[0], -shift[1]), (-3, -2)), ws).reshape(M, C)
-    y = F.linear(xw, w.float()) + b.float()
-    q, k, v = y.split(C, dim=-1)
-    q = ref.rms_norm(q.reshape(M, heads, hd), qn.float(), eps).reshape(M, C)
-    k = ref.rms_norm(k.reshape(M, heads, hd), kn.float(), eps).reshape(M, C)
-    want = torch.cat([q, k, v], -1)
-    nW = B * (H // ws[0]) * (W // ws[1])
-    assert got.shape == (nW, T * ws[0] * ws[1], 3 * C) and got.dtype == dtype
-    assert rel_l2(got.reshape(M, 3 * C), want) < TOL[dtype]
-    # and the unfused two-kernel composition
-    xw2 = ops.rmsnorm_roll_partition(d(x), d(n1), ws, shift, eps)
-    two = ops.qkv_projection(xw2, d(w), d(b), d(qn), d(kn), heads, eps)
-    assert rel_l2(got, two) < TOL[dtype]
-
-
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("M,N,K", [(64800, 4096, 1024), (1000, 576, 192), (257, 4096, 256), (16, 64, 64)])
-@pytest.mark.parametrize("epi", ["none", "bias", "gelu", "residual"])
-def test_linear_rownorm(device, dtype, M, N, K, epi):
-    from nsw import _lib, ops
-    if dtype == torch.float32 and M * N * K > 3e11:
-        pytest.skip("fp32 CPU oracle too slow at this size")
-    g = torch.Generator().manual_seed(M + N + K)
-    x = (2.0 * torch.randn(M, K, generator=g) - 0.3).to(dtype)
-    nw = (1 + 0.2 * torch.randn(K, generator=g)).to(dtype)
-    w = synth.trunc_normal((N, K), 0.02, g).to(dtype)
-    b = (0.1 * torch.randn(N, generator=g)).to(dtype)
-    r = torch.randn(M, N, generator=g).to(dtype)
-    eps = torch.finfo(dtype).eps
-    code = {"none": _lib.NSW_EPI_NONE, "bias": _lib.NSW_EPI_BIAS, "gelu": _lib.NSW_EPI_BIAS_GELU,
-            "residual": _lib.NSW_EPI_BIAS_RESIDUAL}[epi]
-    d = lambda t: t.to(device)
-    got = ops.linear_rownorm(d(x), d(fold(w, nw, dtype)), None if epi == "none" else d(b),
-                             d(r) if epi == "residual" else None, epilogue=code, eps=eps)
-    y = F.linear(ref.rms_norm(x.float(), nw.float(), eps), w.float())
-    if epi != "none":
-        y = y + b.float()
-    if epi == "gelu":
-        y = ref.gelu_erf(y)
-    if epi == "residual":
-        y = y + r.float()
-    assert got.dtype == dtype
-    assert rel_l2(got, y) < TOL[dtype]
 
 
 def segment_sumsq(y, seg):
@@ -190,8 +122,8 @@ def test_linear_rowscale_rejects_bad_partials(device):
 def test_block_norm_folds(device, dtype, case):
     """Block.forward with norm2 folded (6 launches: norm1 gather, proj
     scatter; the default), both norms folded (the one-block window-order
-    chain, 6), norm1 folded into the gathering QKV GEMM (norm2 as a pass) and
-    neither (7) matches the oracle."""
+    chain, 6; fold_norm1 alone selects it too) and neither (7) matches the
+    oracle."""
     import nsw
     B, T, H, W, C, heads, ws, shift = case
     p = synth.block_params(C, heads, seed=41, random_bias=True, random_norm=True)

@@ -80,6 +80,21 @@ def ref_linear(x, w, device):
     return F.linear(x.to(device).float(), w.to(device).float()).cpu()
 
 
+# K an odd number of MFMA steps (32 bf16 / 16 fp32 elements each): the last
+# operand stage holds one step's k and its second half is never consumed
+ODD_K_SHAPES = [
+    (torch.bfloat16, 777, 96, 32), (torch.bfloat16, 513, 128, 96), (torch.bfloat16, 300, 64, 160),
+    (torch.bfloat16, 1000, 256, 2080), (torch.bfloat16, 64800, 128, 32),
+    (torch.float32, 777, 96, 16), (torch.float32, 513, 128, 48), (torch.float32, 300, 64, 80),
+]
+
+
+@pytest.mark.parametrize("dtype,M,N,K", ODD_K_SHAPES)
+@pytest.mark.parametrize("epi", ["none", "bias", "gelu", "residual"])
+def test_linear_odd_k_steps(device, dtype, M, N, K, epi):
+    test_linear_epilogues(device, dtype, M, N, K, epi)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
 @pytest.mark.parametrize("epi", ["none", "bias", "gelu", "residual"])
@@ -131,24 +146,25 @@ def test_qkv_projection_headnorm(device, dtype, M, C, heads):
     assert rel_l2(got, want) < TOL[dtype]
 
 
-def test_qkv_projection_headnorm_c32_fp32(device):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_qkv_projection_headnorm_c32(device, dtype):
     """C = 32 with 8 heads (head dim 4), the width of the reference's model
-    test (tests/test_all.py); fp32 only (bf16 GEMMs take K in multiples of 64)."""
+    test (tests/test_all.py:168-169); in bf16 the GEMM's k is one MFMA step."""
     from nsw import ops
     M, C, heads, hd = 777, 32, 8, 4
     g = torch.Generator().manual_seed(9)
-    x = torch.randn(M, C, generator=g)
-    w = synth.trunc_normal((3 * C, C), 0.02, g)
-    b = 0.1 * torch.randn(3 * C, generator=g)
-    qn = 1 + 0.2 * torch.randn(hd, generator=g)
-    kn = 1 + 0.2 * torch.randn(hd, generator=g)
-    eps = torch.finfo(torch.float32).eps
+    x = torch.randn(M, C, generator=g).to(dtype)
+    w = synth.trunc_normal((3 * C, C), 0.02, g).to(dtype)
+    b = (0.1 * torch.randn(3 * C, generator=g)).to(dtype)
+    qn = (1 + 0.2 * torch.randn(hd, generator=g)).to(dtype)
+    kn = (1 + 0.2 * torch.randn(hd, generator=g)).to(dtype)
+    eps = torch.finfo(dtype).eps
     got = ops.qkv_projection(x.to(device), w.to(device), b.to(device), qn.to(device), kn.to(device), heads, eps)
-    y = ref_linear(x, w, device) + b
+    y = ref_linear(x, w, device) + b.float()
     q, k, v = y.split(C, dim=-1)
-    q = ref.rms_norm(q.reshape(M, heads, hd), qn, eps).reshape(M, C)
-    k = ref.rms_norm(k.reshape(M, heads, hd), kn, eps).reshape(M, C)
-    assert rel_l2(got, torch.cat([q, k, v], -1)) < TOL[torch.float32]
+    q = ref.rms_norm(q.reshape(M, heads, hd), qn.float(), eps).reshape(M, C)
+    k = ref.rms_norm(k.reshape(M, heads, hd), kn.float(), eps).reshape(M, C)
+    assert rel_l2(got, torch.cat([q, k, v], -1)) < TOL[dtype]
 
 
 def attention_oracle(qkv, heads, scale, mask):

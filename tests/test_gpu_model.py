@@ -176,9 +176,11 @@ MODEL_CASES = [
     (2, 2, 6, 6, 36, 72, 2, 64, 4, (9, 18), 2, True),
     (1, 1, 8, 6, 36, 72, 4, 128, 2, (3, 6), 3, False),
     (1, 2, 8, 8, 18, 36, 1, 64, 2, (9, 18), 2, True),
-    # the reference's model test (tests/test_all.py): 720 x 1440, p4, window
-    # 9 x 18, e32 with 8 heads (head dim 4), depth 2, T = 2
-    (1, 2, 4, 4, 720, 1440, 4, 32, 8, (9, 18), 2, True),
+    # the reference's model test (tests/test_all.py:165-171): batch 4, T = 2,
+    # 720 x 1440, p4, window 9 x 18, 20 channels, e32 with 8 heads (head dim
+    # 4), depth 2, learned and coordinate positional embeddings
+    (4, 2, 20, 20, 720, 1440, 4, 32, 8, (9, 18), 2, False),
+    (4, 2, 20, 20, 720, 1440, 4, 32, 8, (9, 18), 2, True),
 ]
 
 
@@ -238,6 +240,9 @@ BF16_CASES = [
     # bf16 MFMA attention head dims (32, 64)
     (2, 2, 6, 6, 36, 72, 2, 128, 4, (9, 18), 2, True),
     (1, 1, 8, 6, 36, 72, 4, 128, 2, (3, 6), 3, False),
+    # the reference's model test model (tests/test_all.py:168-169) in bf16:
+    # e32 (a GEMM k of one 32-element MFMA step), head dim 4
+    (1, 2, 20, 20, 720, 1440, 4, 32, 8, (9, 18), 2, False),
 ]
 
 

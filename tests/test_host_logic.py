@@ -189,3 +189,40 @@ def test_bench_refuses_more_than_one_gpu():
     assert r.returncode == 2, r.stderr
     line = json.loads(r.stdout.strip().splitlines()[-1])
     assert line["n_gpus"] == 2 and "one GPU" in line["error"]
+
+
+def test_workspace_cache_keeps_buffers_a_capture_has_seen(monkeypatch):
+    """The per-stream workspace grows by replacement; a buffer handed out
+    while the stream was being captured into a graph stays alive after it is
+    replaced (replays still write it), any other one is released."""
+    import gc
+    import weakref
+    from nsw import ops
+
+    class _Stream:
+        cuda_stream = 12345
+
+    capturing = [False]
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: _Stream())
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: capturing[0])
+    monkeypatch.setattr(ops, "_workspaces", {})
+    monkeypatch.setattr(ops, "_ws_retired", [])
+    dev = torch.device("cpu")
+
+    a = ops.workspace(100, dev)
+    assert ops.workspace(64, dev) is a                 # smaller: same buffer
+    ra = weakref.ref(a)
+    del a
+    b = ops.workspace(200, dev)                        # grows: the uncaptured buffer goes
+    gc.collect()
+    assert ra() is None and b.numel() >= 200
+
+    capturing[0] = True
+    assert ops.workspace(150, dev) is b                # handed out under capture
+    capturing[0] = False
+    rb = weakref.ref(b)
+    del b
+    c = ops.workspace(400, dev)                        # grows: the captured one is retired, kept
+    gc.collect()
+    assert rb() is not None and any(t is rb() for t in ops._ws_retired)
+    assert c.numel() >= 400 and ops.workspace(400, dev) is c

@@ -88,6 +88,11 @@ def test_validation_errors_without_gpu(L):
     prm = _lib.BlockParams()
     rc = L.nsw_swin_block_forward(16, 16, ctypes.byref(prm), ctypes.byref(shp), 16, 1 << 30, None)
     assert rc == _lib.NSW_ERR_INVALID and b"alias" in L.nsw_last_error()
+    # block: norm1 folded without norm2 (the window-order chain needs both)
+    prm = _lib.BlockParams()
+    prm.wqkv_n1 = 16
+    rc = L.nsw_swin_block_forward(16, 32, ctypes.byref(prm), ctypes.byref(shp), 16, 1 << 40, None)
+    assert rc == _lib.NSW_ERR_INVALID and b"w1_n2" in L.nsw_last_error()
 
 
 def test_blocks_chain_validation_without_gpu(L):
