@@ -1,6 +1,6 @@
 """Coefficients of gelu_erf_bf16 (nsw_gemm_common.h): a least-squares fit
 on Chebyshev nodes of log2(Phi(-a)), Phi the standard normal CDF, on
-[0, 5.5] by a degree-7 polynomial in a, converted to monomial coefficients
+[0, 5.5] by a degree-5 polynomial in a, converted to monomial coefficients
 and rounded to float32.  Run as a script it prints them (low order first)
 and the worst error of the float32 Horner evaluation against float64 GELU
 on a dense grid, in units of the bfloat16 half-ulp of the exact value.
@@ -9,7 +9,7 @@ GELU(v) = v Phi(v) = max(v, 0) - |v| Phi(-|v|), and Phi(-a) = exp2(P(a)).
 """
 import numpy as np
 
-DEGREE = 7
+DEGREE = 5
 RANGE = 5.5
 
 
@@ -41,7 +41,7 @@ def bf16_half_ulp(x: np.ndarray) -> np.ndarray:
 if __name__ == "__main__":
     from scipy.special import ndtr
     coef = fit()
-    print("coefficients (a^0 .. a^7):", ", ".join(f"{float(c):.9e}f" for c in coef))
+    print(f"coefficients (a^0 .. a^{DEGREE}):", ", ".join(f"{float(c):.9e}f" for c in coef))
     v = np.linspace(-12, 12, 2_400_001).astype(np.float32)
     exact = v.astype(np.float64) * ndtr(v.astype(np.float64))
     got = gelu_fast_f32(v, coef).astype(np.float64)

@@ -87,22 +87,21 @@ __device__ __forceinline__ float gelu_erf(float v) {
 }
 
 // Exact-erf GELU for bfloat16 outputs: GELU(v) = max(v, 0) - |v| Phi(-|v|)
-// with Phi(-a) = exp2(P(a)), P a degree-7 least-squares fit of log2 Phi(-a)
+// with Phi(-a) = exp2(P(a)), P a degree-5 least-squares fit of log2 Phi(-a)
 // on [0, 5.5] (csrc/gelu_fit.py, which prints the coefficients and the
-// error).  Worst error on a dense grid of [-12, 12] against float64:
-// 0.0022 of the bfloat16 half-ulp of the exact value (|GELU| >= 2^-24); P
-// keeps decreasing past 5.5, so the tail only shrinks.  10 VALU
-// instructions, one transcendental (v_exp_f32), against 13 and two for
-// gelu_erf, which stays the form for fp32 outputs.
+// error).  Worst error on a dense grid of [-12, 12] against float64: 0.145
+// of the bfloat16 half-ulp of the exact value (|GELU| >= 2^-24; about 0.13
+// throughout v < 1, below 0.02 for v > 1); P keeps decreasing past 5.5, so
+// the tail only shrinks.  8 VALU instructions, one transcendental
+// (v_exp_f32), against 13 and two for gelu_erf, which stays the form for
+// fp32 outputs.
 __device__ __forceinline__ float gelu_erf_bf16(float v) {
   const float a = fabsf(v);
-  float p = fmaf(-1.921197509e-06f, a, 6.328771997e-05f);
-  p = fmaf(p, a, -9.434143431e-04f);
-  p = fmaf(p, a, 8.556244895e-03f);
-  p = fmaf(p, a, -5.405221879e-02f);
-  p = fmaf(p, a, -4.583818614e-01f);
-  p = fmaf(p, a, -1.151278257e+00f);
-  p = fmaf(p, a, -9.999938607e-01f);
+  float p = fmaf(-2.297039027e-04f, a, 4.821910989e-03f);
+  p = fmaf(p, a, -4.437467828e-02f);
+  p = fmaf(p, a, -4.701045752e-01f);
+  p = fmaf(p, a, -1.145988584e+00f);
+  p = fmaf(p, a, -1.000384808e+00f);
   return fmaf(-a, __builtin_amdgcn_exp2f(p), fmaxf(v, 0.0f));
 }
 

