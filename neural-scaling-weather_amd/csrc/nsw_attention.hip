@@ -311,8 +311,8 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
 // ------------------------------------------- bf16 MFMA, direct-to-LDS ----
 // K and V rows of a (window, head) item are copied straight into LDS with
 // buffer_load ... lds, row-major (128 B per row for head dim 64), their
-// 16-byte chunks XOR-swizzled by row (sw_chunk; conflict-free fragment
-// reads, as k_chunk).  The PV product reads its V^T fragments with
+// 16-byte chunks XOR-swizzled by row (K: sw_chunk, conflict-free fragment
+// reads, as k_chunk; V: v_chunk, below).  The PV product reads its V^T fragments with
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i%4
 // of the 4-element vectors addressed by lanes i/4, 4 + i/4, 8 + i/4 and
 // 12 + i/4, so lanes addressing rows 4g + i/4 at dims 16 db + 4 (i%4) yield
@@ -320,6 +320,19 @@ __global__ __launch_bounds__(256, 3) void attn_mfma_kernel(AttnArgs a) {
 // keys {4g+r, 16+4g+r}, the key order of the probability registers.
 __device__ __forceinline__ int sw_chunk(int row, int ch) {
   return ch ^ (((row >> 1) & 7) ^ ((row & 1) << 2));
+}
+
+// Chunk placement of the V rows.  A transposing read of the PV product
+// covers, per 32-lane half of the wave, 8 consecutive rows 8i .. 8i + 7 at
+// the two chunks 2 db, 2 db + 1 (per 16-lane quarter, 4 consecutive rows).
+// Rows of equal parity share the 128-byte bank half, so chunk c of row r
+// sits at c ^ 2 f(r), f(r) = ((r >> 1) & 3) ^ 2 (r & 1): f is distinct on
+// the four rows of either parity in 8 consecutive rows and on 4 consecutive
+// rows, so both halves' and all quarters' 16 chunk pairs fall in distinct
+// banks (with sw_chunk the even rows 2 apart collided: 2-way conflicts on
+// every V^T read).
+__device__ __forceinline__ int v_chunk(int row, int ch) {
+  return ch ^ (2 * (((row >> 1) & 3) ^ ((row & 1) << 1)));
 }
 
 // The resource built from kernel arguments, pinned to SGPRs (the inline asm
@@ -338,7 +351,7 @@ __device__ __forceinline__ void store16_asm(const u32x4& rsrc, uint32_t voff, co
 }
 
 // One 16-query block of a (window, head) item with head dim 64: K rows and V
-// rows (KP of each, 128 B per row, 16-byte chunks placed by sw_chunk) in LDS,
+// rows (KP of each, 128 B per row, 16-byte chunks placed by sw_chunk / v_chunk) in LDS,
 // V rows past L zero (so that their zero probabilities give exact zeros), the
 // block's Q fragments in registers.  Computes S^T = K Q^T, the masked
 // softmax in the exp2 domain (row max by permlane reduction, row sums by an
@@ -425,9 +438,9 @@ __device__ __forceinline__ void attn_qblock64(const AttnArgs& a, const char* Ks,
       const int lc = 2 * db + (fr & 3) / 2;
       const int half = (fr & 1) * 8;
       const i16x4 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s4*)(Vs + r0 * 128 + sw_chunk(r0, lc) * 16 + half));
+          (lds_s4*)(Vs + r0 * 128 + v_chunk(r0, lc) * 16 + half));
       const i16x4 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s4*)(Vs + (r0 + 16) * 128 + sw_chunk(r0 + 16, lc) * 16 + half));
+          (lds_s4*)(Vs + (r0 + 16) * 128 + v_chunk(r0 + 16, lc) * 16 + half));
       const bf16x4 l4 = __builtin_bit_cast(bf16x4, lo4), h4 = __builtin_bit_cast(bf16x4, hi4);
       vf[b][db] = bf16x8{l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
     }
@@ -468,7 +481,7 @@ __device__ __forceinline__ void attn_qblock64(const AttnArgs& a, const char* Ks,
 
 // One workgroup per (window, head) item, head dim 64, shift mask from indices
 // or none (three workgroups per CU).  K and V rows go straight to LDS with
-// buffer_load ... lds (row-major, chunks placed by sw_chunk: no VGPR staging,
+// buffer_load ... lds (row-major, chunks placed by sw_chunk / v_chunk: no VGPR staging,
 // no transposing LDS writes); each wave's Q fragments are loaded into
 // registers alongside.  Waves take query blocks wave, wave + 4, ...
 template <int NKB>
@@ -515,7 +528,7 @@ __global__ __launch_bounds__(256, 3) void attn_dma_kernel(AttnArgs a, int nitems
     const int d = wave * NDMA + j;
     const int part = d / RG, rg = d - part * RG;
     const int row = rg * 8 + lane / 8;
-    const int lc = sw_chunk(row, lane % 8);
+    const int lc = part == 0 ? sw_chunk(row, lane % 8) : v_chunk(row, lane % 8);
     // V rows past L read from offset qkv_bytes, past the end of qkv: the
     // range check returns zeros, which land in LDS as the padding rows
     const uint32_t voff = part == 1 && row >= L
