@@ -19,8 +19,8 @@ The line also carries
               forward of the depth-8 p2 model;
   "shard":    one GPU's share of config 2 split 2-way in longitude (the
               block on 180 x 180 tokens), time per token against the full block;
-  "achievable": this box's own peaks, the better of a 1 GiB read-only pass
-              and a 1 GiB device copy (HBM), and the fastest hipBLASLt GEMM
+  "achievable": this box's own peaks, the best of a 1 GiB read-only stream
+              and 1 GiB device copies (HBM), and the fastest hipBLASLt GEMM
               of an 8192^3 product and the block's four shapes (MFMA); every
               kernel entry and the roofline also give frac_achievable, the
               fraction of those beside the fraction of the spec peaks;
@@ -538,16 +538,27 @@ def metrics_timing(dev, steps, warmup):
 
 def achievable_peaks(dev, dtype, steps, warmup, gemms=None):
     """What this box reaches on its own, the references of the per-kernel
-    frac_achievable: HBM, the better of a read-only pass (torch.sum over
-    1 GiB) and a 1 GiB device-to-device copy (bytes read + written); MFMA,
-    the fastest of an 8192^3 torch.matmul in the block's dtype and the
-    block's own four GEMM shapes through torch.matmul (``gemms``, the
-    gemm_vs_hipblaslt leg), all hipBLASLt."""
+    frac_achievable: HBM, the best of a read-only stream over 1 GiB (this
+    library's nsw_hbm_stream probe, read bytes), the probe's 1 GiB copy and
+    torch's 1 GiB copy_ (read + write bytes); MFMA, the fastest of an 8192^3
+    torch.matmul in the block's dtype and the block's own four GEMM shapes
+    through torch.matmul (``gemms``, the gemm_vs_hipblaslt leg), all
+    hipBLASLt."""
     import torch
+    from nsw import _lib
     n = 1 << 28
     src = torch.ones(n, dtype=torch.float32, device=dev)
-    t_read = timed(lambda: src.sum(), steps, warmup)
     dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    L = _lib.lib()
+
+    def probe(d):
+        rc = L.nsw_hbm_stream(src.data_ptr(), d, 4 * n, 0, stream)
+        if rc != 0:
+            raise RuntimeError(L.nsw_last_error().decode())
+
+    t_read = timed(lambda: probe(None), steps, warmup)
+    t_pcopy = timed(lambda: probe(dst.data_ptr()), steps, warmup)
     t_copy = timed(lambda: dst.copy_(src), steps, warmup)
     del src, dst
     N = 8192
@@ -557,15 +568,17 @@ def achievable_peaks(dev, dtype, steps, warmup, gemms=None):
     t_mm = timed(lambda: torch.matmul(a, b), steps, warmup)
     del a, b
     read_gbs = n * 4 / (t_read * 1e-3) / 1e9
+    pcopy_gbs = 2 * n * 4 / (t_pcopy * 1e-3) / 1e9
     copy_gbs = 2 * n * 4 / (t_copy * 1e-3) / 1e9
     mm = {f"matmul {N}^3": 2.0 * N ** 3 / (t_mm * 1e-3) / 1e12}
     for name, r in (gemms or {}).items():
         mm[f"{name} shape"] = r["hipblaslt_tflops"]
     best = max(mm, key=mm.get)
-    return {"hbm_GBs": round(max(read_gbs, copy_gbs), 1), "hbm_read_GBs": round(read_gbs, 1),
-            "hbm_copy_GBs": round(copy_gbs, 1), "mfma_tflops": round(mm[best], 1),
+    return {"hbm_GBs": round(max(read_gbs, pcopy_gbs, copy_gbs), 1), "hbm_read_GBs": round(read_gbs, 1),
+            "hbm_copy_GBs": round(max(pcopy_gbs, copy_gbs), 1), "mfma_tflops": round(mm[best], 1),
             "mfma_source": f"hipBLASLt {best} ({str(dtype).replace('torch.', '')})",
-            "hbm": "max of torch.sum over 1 GiB fp32 (read bytes) and a 1 GiB copy_ (read + write bytes)",
+            "hbm": "best of a 1 GiB read-only stream (nsw_hbm_stream, read bytes) and 1 GiB copies "
+                   "(nsw_hbm_stream, torch copy_; read + write bytes)",
             "gemm_tflops": {k: round(v, 1) for k, v in mm.items()}}
 
 

@@ -384,6 +384,15 @@ int nsw_head_unpatchify(const void* x, const void* w_perm, void* out, int64_t B,
                         int64_t W, int64_t p, int64_t K, int64_t out_bstride, int dtype, int out_dtype,
                         void* stream);
 
+/* HBM stream probe.  No counterpart in the reference: a measurement helper
+ * for callers that report kernel rates against what the device sustains
+ * (bench.py's achievable peaks).  dst == NULL: reads `bytes` from src with
+ * 16-byte loads, four per lane in flight (their bits are folded into a
+ * checksum that touches nothing outside the library); otherwise copies
+ * `bytes` from src to dst.  bytes a multiple of 16, src / dst 16-byte
+ * aligned; blocks = 0 picks 16384 workgroups of 256 threads. */
+int nsw_hbm_stream(const void* src, void* dst, int64_t bytes, int64_t blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,48 +32,68 @@ __device__ __forceinline__ int64_t src_row(int64_t m, const WinGeom& g) {
   }
 }
 
-// One wave per row; CH = number of 16-byte chunks per lane (C <= 64*CH*VEC).
-template <typename T, int MAP, bool NORM, int CH>
+// RPW rows per wave; CH = number of 16-byte chunks per lane (C <= 64*CH*VEC).
+// A wave issues the loads of all its rows (and the norm weight, shared by
+// them) before any arithmetic, so that RPW * CH 16-byte loads per lane are in
+// flight; the row sums of squares are reduced with DPP and permlane swaps.
+template <typename T, int MAP, bool NORM, int CH, int RPW>
 __global__ __launch_bounds__(256) void row_map_kernel(const T* __restrict__ x,
                                                       const T* __restrict__ w, float eps,
                                                       T* __restrict__ y, int64_t rows, int C,
                                                       WinGeom g) {
   constexpr int VEC = Vec16<T>::N;
   const int lane = threadIdx.x & 63;
-  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (m >= rows) return;
-  const int64_t s = src_row<MAP>(m, g);
-  const T* xr = x + s * C;
-  T* yr = y + m * C;
-  float v[CH][VEC];
-  float ss = 0.f;
+  const int64_t m0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  if (m0 >= rows) return;
+  float wv[NORM ? CH : 1][VEC];
+  if constexpr (NORM) {
 #pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    const int c0 = (lane + 64 * k) * VEC;
-    if (c0 < C) {
-      load16<T>(xr + c0, v[k]);
-      if constexpr (NORM) {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) ss += v[k][e] * v[k][e];
-      }
+    for (int k = 0; k < CH; ++k) {
+      const int c0 = (lane + 64 * k) * VEC;
+      if (c0 < C) load16<T>(w + c0, wv[k]);
     }
   }
-  float rs = 1.f;
-  if constexpr (NORM) {
-    ss = wave_sum(ss);
-    rs = 1.0f / sqrtf(ss / (float)C + eps);
+  float v[RPW][CH][VEC];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t m = m0 + r < rows ? m0 + r : rows - 1;   // a tail row re-reads the last row (not stored)
+    const T* xr = x + src_row<MAP>(m, g) * C;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int c0 = (lane + 64 * k) * VEC;
+      if (c0 < C) load16<T>(xr + c0, v[r][k]);
+    }
   }
 #pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    const int c0 = (lane + 64 * k) * VEC;
-    if (c0 < C) {
-      if constexpr (NORM) {
-        float wv[VEC];
-        load16<T>(w + c0, wv);
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t m = m0 + r;
+    float rs = 1.f;
+    if constexpr (NORM) {
+      float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) v[k][e] = (v[k][e] * rs) * wv[e];
+      for (int k = 0; k < CH; ++k) {
+        const int c0 = (lane + 64 * k) * VEC;
+        if (c0 < C) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) ss += v[r][k][e] * v[r][k][e];
+        }
       }
-      store16<T>(yr + c0, v[k]);
+      ss = rows4_sum(row16_sum(ss));
+      rs = 1.0f / sqrtf(ss / (float)C + eps);
+    }
+    if (m < rows) {
+      T* yr = y + m * C;
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        const int c0 = (lane + 64 * k) * VEC;
+        if (c0 < C) {
+          if constexpr (NORM) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) v[r][k][e] = (v[r][k][e] * rs) * wv[k][e];
+          }
+          store16<T>(yr + c0, v[r][k]);
+        }
+      }
     }
   }
 }
@@ -122,20 +142,24 @@ static int launch_row_map(const void* x, const void* w, float eps, void* y, int6
                 "%s: pointers must be 16-byte aligned", what);
   if (rows == 0) return NSW_OK;
   const int64_t per_lane = (C / VEC + 63) / 64;
-  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   const T* xp = (const T*)x;
   const T* wp = (const T*)w;
   T* yp = (T*)y;
+  // rows of one chunk per lane (up to 1 KB: C <= 512 in bf16) go two to a
+  // wave (config 4's gather: 95.3 -> 89.9 us standalone); longer rows one
+  // to a wave (two were slower at C = 1024: 42.4 against 39.9 us)
+  auto grid = [&](int rpw) { return dim3((unsigned)((rows + 4 * rpw - 1) / (4 * rpw))); };
+  const dim3 block(256);
   if (per_lane <= 1)
-    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 1>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 1, 2>), grid(2), block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
   else if (per_lane <= 2)
-    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 2>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 2, 1>), grid(1), block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
   else if (per_lane <= 4)
-    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 4>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 4, 1>), grid(1), block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
   else if (per_lane <= 8)
-    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 8>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 8, 1>), grid(1), block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
   else if (per_lane <= 16)
-    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 16>), grid, block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
+    hipLaunchKernelGGL((row_map_kernel<T, MAP, NORM, 16, 1>), grid(1), block, 0, st, xp, wp, eps, yp, rows, (int)C, g);
   else
     return set_error(NSW_ERR_UNSUPPORTED, "%s: C=%lld too large (max %d)", what, (long long)C, 64 * 16 * VEC);
   return check_launch(what);

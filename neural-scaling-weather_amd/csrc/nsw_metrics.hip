@@ -66,7 +66,64 @@ __global__ __launch_bounds__(256) void wsum_partial_kernel(const TP* __restrict_
       s3 += w * ao * ao;
     }
   };
-  if constexpr (VEC4) {
+  if constexpr (VEC4 && !FULLW) {
+    // One latitude row per wave at a time (rows h0 + wave, + 4, ...): the
+    // row's weight is wave-uniform, and the four sums are accumulated per
+    // lane without it in float64 and scaled by it once per row.  Each lane
+    // keeps U 16-byte vectors of each field in flight (W <= 64 U 4 in one
+    // pass).
+    constexpr int U = 6;
+    const int wq = W >> 2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int h = h0 + wave; h < h1; h += 4) {
+      const TP* pr = pp + (int64_t)h * W;
+      const float* tr = tp + (int64_t)h * W;
+      double r0 = 0.0, r1 = 0.0, r2 = 0.0, r3 = 0.0;
+      for (int f0 = 0; f0 < wq; f0 += 64 * U) {
+        float p[U][4];
+        f32x4 t[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int f = f0 + u * 64 + lane;
+          if (f < wq) {
+            load4<TP>(pr + 4 * f, p[u]);
+            t[u] = *reinterpret_cast<const f32x4*>(tr + 4 * f);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int f = f0 + u * 64 + lane;
+          if (f < wq) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              TS pv = (TS)p[u][e], tv = (TS)t[u][e];
+              if constexpr (AFFINE) {
+#pragma clang fp contract(off)
+                pv = pv * sc + of;
+                tv = tv * sc + of;
+              }
+              const TS d = pv - tv;
+              const TS d2 = d * d;
+              r0 += (double)d2;
+              if constexpr (ACC) {
+                const double af = (double)(pv - cl), ao = (double)(tv - cl);
+                r1 = fma(af, ao, r1);
+                r2 = fma(af, af, r2);
+                r3 = fma(ao, ao, r3);
+              }
+            }
+          }
+        }
+      }
+      const double w = wlat[h];
+      s0 = fma(w, r0, s0);
+      if constexpr (ACC) {
+        s1 = fma(w, r1, s1);
+        s2 = fma(w, r2, s2);
+        s3 = fma(w, r3, s3);
+      }
+    }
+  } else if constexpr (VEC4) {
     // The band's rows are contiguous in the plane: n4 vectors of 4 from row
     // h0 on.  Each thread keeps U vector loads of each field in flight (the
     // loads of a group are issued before its arithmetic); the row of vector
@@ -317,4 +374,67 @@ extern "C" int nsw_weighted_metrics_unnorm_noalloc(const void* pred, int pred_dt
     return run_metrics<bf16, float, true>((const bf16*)pred, target, w, w_cols, clim, std_c, mean_c, P, H, W,
                                           Cch, rmse, acc, ptr, NSW_METRICS_SCRATCH_BYTES, st, what);
   return set_error(NSW_ERR_INVALID, "%s: unknown dtype %d", what, pred_dtype);
+}
+
+// ------------------------------------------------------ HBM stream probe ----
+// nsw_hbm_stream: a grid-stride pass over `bytes` with four 16-byte loads per
+// lane in flight (the loads of a group are issued before any use), read-only
+// or copying; the read-only form keeps its loads by folding them into an
+// xor of their bits, stored into a device global only when it equals one
+// particular value (harmless either way: the global is the probe's own).
+namespace nsw {
+
+__device__ uint32_t nsw_hbm_probe_sink;   // external linkage: its stores stay
+
+__global__ __launch_bounds__(256) void hbm_read_kernel(const u32x4* __restrict__ p, int64_t n) {
+  constexpr int U = 4;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const int64_t stride = (int64_t)gridDim.x * 256 * U;
+  for (int64_t i = (int64_t)blockIdx.x * 256 * U + threadIdx.x; i < n; i += stride) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = i + u * 256;
+      v[u] = j < n ? p[j] : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u];
+  }
+  const uint32_t s = (acc[0] ^ acc[1]) ^ (acc[2] ^ acc[3]);
+  if (s == 0x9e3779b9u) nsw_hbm_probe_sink = s;
+}
+
+__global__ __launch_bounds__(256) void hbm_copy_kernel(const f32x4* __restrict__ p, f32x4* __restrict__ q,
+                                                       int64_t n) {
+  constexpr int U = 4;
+  const int64_t stride = (int64_t)gridDim.x * 256 * U;
+  for (int64_t i = (int64_t)blockIdx.x * 256 * U + threadIdx.x; i < n; i += stride) {
+    f32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = i + u * 256;
+      if (j < n) v[u] = p[j];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = i + u * 256;
+      if (j < n) q[j] = v[u];
+    }
+  }
+}
+
+}  // namespace nsw
+
+extern "C" int nsw_hbm_stream(const void* src, void* dst, int64_t bytes, int64_t blocks, void* stream) {
+  const char* what = "nsw_hbm_stream";
+  NSW_CHECK_ARG(src != nullptr && bytes > 0 && bytes % 16 == 0, "%s: src and a positive multiple of 16 bytes", what);
+  NSW_CHECK_ARG(((uintptr_t)src % 16) == 0 && ((uintptr_t)dst % 16) == 0, "%s: 16-byte aligned pointers", what);
+  NSW_CHECK_ARG(blocks >= 0 && blocks < (1LL << 31), "%s: blocks out of range", what);
+  const unsigned nb = blocks > 0 ? (unsigned)blocks : 16384u;
+  hipStream_t st = (hipStream_t)stream;
+  if (dst == nullptr)
+    hipLaunchKernelGGL(hbm_read_kernel, dim3(nb), dim3(256), 0, st, (const u32x4*)src, bytes / 16);
+  else
+    hipLaunchKernelGGL(hbm_copy_kernel, dim3(nb), dim3(256), 0, st, (const f32x4*)src, (f32x4*)dst, bytes / 16);
+  return check_launch(what);
 }

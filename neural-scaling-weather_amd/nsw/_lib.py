@@ -86,6 +86,7 @@ SIGNATURES = {
                                                     _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
     "nsw_weighted_metrics_unnorm_noalloc": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
                                                    _i64, _vp, _vp, _vp]),
+    "nsw_hbm_stream": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "nsw_linear_rowscale": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _f32, _int,
                                    _vp]),
     "nsw_row_sumsq_parts": (_i64, [_i64, _int]),
