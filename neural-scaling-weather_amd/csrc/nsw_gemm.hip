@@ -110,32 +110,41 @@ __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk)
 
 // Main loop of the 256 x 256 tile.  Stage st holds 128 bytes of k of the 256
 // x rows and the 256 w rows.  x lives in a ring of 3 slots and w in a ring of
-// 2 slots of 32 KB (160 KB in all), so that the copies of a stage are issued
-// at a steady 4 instructions per wave and MFMA step:
+// 2 slots of 32 KB (160 KB in all).  The copies are issued by the four waves
+// of the first row half (waves 0-3, one per SIMD: NC = 8 copies of each
+// operand per stage each, 64 rows); the other four waves run only LDS reads
+// and MFMAs, so that on every SIMD one wave's MFMA stream is free of copy
+// issue (bit-identical; 2-5% faster on the block's four GEMM shapes than
+// 4 + 4 copies per wave, measured on one box; the copies on waves 4-7
+// instead were 2-5% slower than 4 + 4).  A copying wave issues its copies of
+// a step in the step's first two n blocks (4 each):
 //   step 2s+1 (the second step of stage s, after the barrier that frees the
 //              slots of stage s): w of stage s+2 into w slot s%2;
 //   step 2s+2 (the first step of stage s+1): x of stage s+3 into x slot s%3,
 // and the x copies (the operand with fewer sharers in L2) get 2-3 steps of
-// lead, the w copies 1-2.  At the start of step 2s+1 a wave waits for the
+// lead, the w copies 1-2.  At the start of step 2s+1 a wave waits for its
 // copies of stage s+1 (only x of stage s+2 may still be in flight), then
 // barrier.  The fragments of step k+1 are read during step k, so a slot is
 // free once the barrier at the start of the last step of its stage has
-// passed.
-template <typename T, int PRE>
+// passed.  NC = 0: a wave that copies nothing (same barriers).
+template <typename T, int PRE, int NC>
 __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X, const T* __restrict__ Wt, int M,
                                              int N, int K, int m0, int n0, const EpiArgs& ea,
                                              f32x4 (&acc)[NB][MB], int wave, int lane) {
   constexpr int SLOT = 256 * ROWB;        // one operand's stage: 32 KB
-  constexpr int NC = SLOT / (NW * 1024);  // copies per wave per operand and stage (4)
-  constexpr int WR = 256 / NW;            // stage rows copied by one wave (32)
+  constexpr int NCA = NC > 0 ? NC : 1;
+  constexpr int WR = NC * 8;              // stage rows copied by one wave (64)
+  constexpr int CG = 2;                   // n blocks of a step that issue its copies
+  constexpr int CPG = NC / CG;            // copies per such n block
   constexpr int UNR = 12;                 // steps per loop iteration: 6 stages, a multiple of 3 and 2
   static_assert(MB == 8 && NB == 4, "the step's schedule assumes 8 x 4 result blocks per wave");
+  static_assert(NC == 0 || (NC % CG == 0 && WR * 4 == 256), "four copying waves cover the 256 stage rows");
   const uint32_t rowbytes = (uint32_t)K * sizeof(T);
   const u32x4 rx = make_rsrc(X, (uint32_t)M * rowbytes);
   const u32x4 rw = make_rsrc(Wt, (uint32_t)N * rowbytes);
   // copy j of this wave covers slot rows wave*WR + 8j .. +7; lane i writes row
   // +i/8, 16-byte slot i%8, and loads global chunk slot ^ swizzle(row)
-  uint32_t vx[NC], vw[NC];
+  uint32_t vx[NCA], vw[NCA];
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
     const int srow = wave * WR + j * 8 + lane / 8;
@@ -211,13 +220,17 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
       const uint32_t wdst_ = cbase + (k + 1 < nk ? NSW_WSLOT(su_ + 2) : NSW_XSLOT(su_ + 1));    \
       const int cst_ = st + 2 < nst ? st + 2 : nst - 1;   /* past the end: the last stage, in L2 */ \
       /* n-block-major: the first MFMAs of a step need only its first weight  */             \
-      /* fragment.  Per n block: one copy, MB/NB next-step x fragments, MB    */             \
-      /* MFMAs, then the next step's weight fragment nb into the registers    */             \
-      /* the MFMAs have just released (two sets of x fragments, one of w)      */             \
+      /* fragment.  Per n block: the copies (first CG blocks), MB/NB next-step */            \
+      /* x fragments, MB MFMAs, then the next step's weight fragment nb into   */            \
+      /* the registers the MFMAs have just released (two sets of x fragments, */             \
+      /* one of w)                                                             */            \
       _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                      \
-        if (nb < NC) {                                                                         \
-          if (sub_ == 1) dma16(rw, wdst_ + nb * 1024, vw[nb], cst_ * ROWB);                    \
-          else NSW_COPY_X(su_ + 2, cst_, nb);                                                  \
+        if (nb < CG) {                                                                         \
+          _Pragma("unroll") for (int c_ = 0; c_ < CPG; ++c_) {                                 \
+            const int j_ = nb * CPG + c_;                                                      \
+            if (sub_ == 1) dma16(rw, wdst_ + j_ * 1024, vw[j_], cst_ * ROWB);                  \
+            else NSW_COPY_X(su_ + 2, cst_, j_);                                                \
+          }                                                                                    \
         }                                                                                      \
         /* unconditional: after the last step these read stale slots (unused); a  */         \
         /* conditional read would make the wait-count pass drain all LDS reads   */         \
@@ -348,7 +361,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
     for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int frow = lane & 15, fg = lane >> 4;
 
-  mainloop_256<T, PRE>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane);
+  // waves 0-3 copy the operands, waves 4-7 do not (see mainloop_256)
+  if (wave < 4) mainloop_256<T, PRE, 8>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane);
+  else mainloop_256<T, PRE, 0>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane);
 
   // ---------------------------------------------------------------- epilogue
   // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
