@@ -121,6 +121,9 @@ def main():
                          "markdown and write profiles/traffic_<config>.json")
     ap.add_argument("--no-config4", action="store_true", help="skip the config-4 block and model timing")
     ap.add_argument("--no-gemm-compare", action="store_true", help="skip the hipBLASLt comparison leg")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="run only the hipBLASLt comparison leg (the block's four GEMM shapes, this library's "
+                         "GEMM against torch.matmul) and print its JSON: the command its counter profiles use")
     ap.add_argument("--no-block-calls", action="store_true",
                     help="skip the config-3 comparison run with one fused call per block (the forward keeps "
                          "the residual stream in window order between blocks)")
@@ -143,6 +146,12 @@ def main():
 
     if args.copy_calibration:
         copy_calibration()
+    if args.gemm_only:
+        B, T, H, W, C = CONFIGS[args.config][:5]
+        M = B * T * H * W
+        print(json.dumps({"gemm_vs_hipblaslt": gemm_compare(torch.device("cuda:0"), M, C, 4 * C, args.steps,
+                                                            args.warmup)}), flush=True)
+        return
 
     B, T, H, W, C, heads, ws, shift, dts, desc = CONFIGS[args.config]
     dtype = torch.bfloat16 if dts == "bf16" else torch.float32
