@@ -680,7 +680,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
             if (!ok) ssq = 0.f;
           }
         } else {
-          if (ok) *reinterpret_cast<u32x4*>(Y + (int64_t)orow[cur][b] * N + n) = ov[b];
+          // non-temporal: the tile is not read again by this kernel, and the
+          // outputs without a residual (qkv, the MLP hidden rows: 398 / 531
+          // MB at config 2) exceed the last-level cache; streaming them past
+          // L2 made these GEMMs 4-5% faster (fc1 504 -> 481 us, bit-identical;
+          // the residual epilogues, whose 133 MB outputs the next kernel
+          // reads, showed no gain and keep ordinary stores)
+          if (ok) __builtin_nontemporal_store(ov[b], reinterpret_cast<u32x4*>(Y + (int64_t)orow[cur][b] * N + n));
         }
         if constexpr (SUMSQ) {
           // partial sum of squares over 32 lanes (32 * VEC columns, one float
