@@ -514,9 +514,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   constexpr int LPR = BN / VEC;                       // lanes per output row (32 bf16 / 64 f32)
   constexpr int RPI = 64 / LPR;                       // rows per copy instruction (2 / 1)
   constexpr int ITER = S::ROWS / NW / RPI;            // copy instructions per wave per pass
-  constexpr int BATCH = ITER < 8 ? ITER : 8;
-  constexpr int NBAT = ITER / BATCH;
-  static_assert(ITER % BATCH == 0, "batch");
+  constexpr int BATCH = 8;                            // rows loaded one batch ahead (at most)
   constexpr bool SCAT = EPI == EPI_SCATTER_RESIDUAL;
   constexpr bool REMAP = EPI == EPI_REMAP_RESIDUAL;
   constexpr bool TOK = EPI == EPI_TOKEN_RESIDUAL;
@@ -570,38 +568,60 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   const int col = (lane % LPR) * VEC;                 // first tile column of this lane
   const int n = n0 + col;
   const int nc = n < N ? n : 0;                       // clamped column for loads
+  // Phases: with the whole tile staged at once (bf16), staging and copy-out
+  // run in NPH phases of MB / NPH row blocks per wave-row half, and a
+  // phase's copy-out (LDS reads, global stores in flight) is followed by
+  // the staging of the next phase's rows, so that the epilogue math (VALU)
+  // overlaps the stores of the rows before it.  Phase p covers the tile
+  // rows [p RHP, (p + 1) RHP) of both wave-row halves; its copy-out gives
+  // each wave 2 RHP / NW consecutive rows of one half.
+  constexpr int NPH = (S::PASSES == 1 && EPI != EPI_UNPATCH) ? 4 : 1;
+  constexpr int IPP = ITER / NPH;                     // copy instructions per wave and phase
+  constexpr int BAT = IPP < BATCH ? IPP : BATCH;      // rows loaded one batch ahead
+  constexpr int NBP = IPP / BAT;                      // batches per phase
+  constexpr int NBT = NPH * NBP;                      // batches per pass
+  constexpr int RHP = WTM / NPH;                      // rows of a wave-row half per phase
+  static_assert(ITER % NPH == 0 && IPP % BAT == 0 && (NPH == 1 || NW * IPP * RPI == 2 * RHP), "phases");
 #pragma unroll
   for (int pass = 0; pass < S::PASSES; ++pass) {
     const int prow0 = pass * S::ROWS;                 // first tile row of this pass
-    int orow[2][BATCH];                               // output row (token for the scatter) per batch row
-    u32x4 rres[2][RES ? BATCH : 1];
+    // tile row of the j-th row of phase p's copy-out (j = wave IPP RPI + ...)
+    auto tile_row = [&](int p, int j) {
+      return prow0 + (NPH == 1 ? j : (j / RHP) * WTM + p * RHP + j % RHP);
+    };
+    int orow[2][BAT];                                 // output row (token for the scatter) per batch row
+    u32x4 rres[2][RES ? BAT : 1];
     float ssacc = 0.f;                                // row sums of squares of the pass (SUMSQ)
-    // Row maps: the wave copies ITER * RPI (<= 64) consecutive rows per pass,
-    // so lane l maps the wave's row l once and every copy instruction takes
-    // its rows' targets from those lanes (v_readlane) instead of all 32 or
-    // 64 lanes of a row evaluating the same map.
+    // Row maps: the wave copies ITER * RPI (<= 64) rows per pass, so lane l
+    // maps the wave's l-th row once and every copy instruction takes its
+    // rows' targets from those lanes (v_readlane) instead of all 32 or 64
+    // lanes of a row evaluating the same map.
     constexpr bool MAPPED = SCAT || TOK || REMAP || TOWIN;
     constexpr int WROWS = ITER * RPI;                 // rows per wave per pass
     static_assert(WROWS <= 64, "one row per lane");
+    // the wave's l-th row (l < WROWS): phase l / (IPP RPI), j = wave IPP RPI + l % (IPP RPI)
+    auto wave_row = [&](int l) { return tile_row(l / (IPP * RPI), wave * IPP * RPI + l % (IPP * RPI)); };
     int lmap = 0;
     if constexpr (MAPPED) {
-      int mm = m0 + prow0 + wave * WROWS + (lane % WROWS);
+      int mm = m0 + wave_row(lane % WROWS);
       mm = mm < M ? mm : M - 1;
       if constexpr (REMAP) lmap = (int)ea.geom.row_of_row_shift(mm, ea.dh, ea.dw);
       else if constexpr (TOWIN) lmap = (int)ea.geom.row_of_token(mm);
       else lmap = (int)ea.geom.token_of_row(mm);
     }
-    auto prefetch = [&](int ib, int slot) {
+    // batch g, row b: phase g / NBP, instruction qq of the phase; its rows
+    // are the wave's rows ql and ql + 1 (bf16) in the order of wave_row
+    auto prefetch = [&](int g, int slot) {
 #pragma unroll
-      for (int b = 0; b < BATCH; ++b) {
-        const int q = ib * BATCH + b;                 // copy instruction of the pass (unrolled: constant)
-        const int rl = (wave * ITER + q) * RPI + lrow;
-        int m = m0 + prow0 + rl;
+      for (int b = 0; b < BAT; ++b) {
+        const int ph = g / NBP, qq = (g % NBP) * BAT + b;
+        const int ql = (ph * IPP + qq) * RPI;         // lane of this instruction's first row
+        int m = m0 + tile_row(ph, wave * IPP * RPI + qq * RPI + lrow);
         m = m < M ? m : M - 1;
         if constexpr (MAPPED) {
-          const int a0 = __builtin_amdgcn_readlane(lmap, q * RPI);
+          const int a0 = __builtin_amdgcn_readlane(lmap, ql);
           if constexpr (RPI == 2) {
-            const int a1 = __builtin_amdgcn_readlane(lmap, q * RPI + 1);
+            const int a1 = __builtin_amdgcn_readlane(lmap, ql + 1);
             orow[slot][b] = lrow ? a1 : a0;
           } else {
             orow[slot][b] = a0;
@@ -615,17 +635,21 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
           rres[slot][b] = *reinterpret_cast<const u32x4*>((const T*)ea.residual + (int64_t)rrow * N + nc);
       }
     };
-    prefetch(0, 0);
+    // epilogue math of phase p's row blocks, stored in the fragment layout
+    auto stage = [&](int p) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int trow = wm * WTM + mb * 16 + frow - prow0;
-      if (wm * WTM + mb * 16 - prow0 >= 0 && wm * WTM + mb * 16 - prow0 < S::ROWS) {   // wave-uniform
-        float v[NB][4];
-        row_values(mb, v);
+      for (int mb = p * (MB / NPH); mb < (p + 1) * (MB / NPH); ++mb) {
+        const int trow = wm * WTM + mb * 16 + frow - prow0;
+        if (wm * WTM + mb * 16 - prow0 >= 0 && wm * WTM + mb * 16 - prow0 < S::ROWS) {   // wave-uniform
+          float v[NB][4];
+          row_values(mb, v);
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) store4<T>(reinterpret_cast<T*>(stg + trow * S::STRIDE) + wn * WTN + nb * 16 + fg * 4, v[nb]);
+          for (int nb = 0; nb < NB; ++nb) store4<T>(reinterpret_cast<T*>(stg + trow * S::STRIDE) + wn * WTN + nb * 16 + fg * 4, v[nb]);
+        }
       }
-    }
+    };
+    prefetch(0, 0);
+    stage(0);
     wg_barrier();
     if constexpr (EPI == EPI_UNPATCH) {
       switch (ea.img_p) {
@@ -639,19 +663,20 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
       continue;
     }
 #pragma unroll
-    for (int ib = 0; ib < NBAT; ++ib) {
-      const int cur = ib & 1;
-      if (ib + 1 < NBAT) prefetch(ib + 1, cur ^ 1);
-      u32x4 ov[BATCH];
+    for (int g = 0; g < NBT; ++g) {
+      const int cur = g & 1;
+      if (g + 1 < NBT) prefetch(g + 1, cur ^ 1);
+      const int ph = g / NBP;
+      u32x4 ov[BAT];
 #pragma unroll
-      for (int b = 0; b < BATCH; ++b) {
-        const int rl = (wave * ITER + ib * BATCH + b) * RPI + lrow;
+      for (int b = 0; b < BAT; ++b) {
+        const int rl = tile_row(ph, wave * IPP * RPI + ((g % NBP) * BAT + b) * RPI + lrow) - prow0;
         ov[b] = *reinterpret_cast<const u32x4*>(stg + rl * S::STRIDE + col * (int)sizeof(T));
       }
 #pragma unroll
-      for (int b = 0; b < BATCH; ++b) {
-        const int rl = (wave * ITER + ib * BATCH + b) * RPI + lrow;
-        const int m = m0 + prow0 + rl;
+      for (int b = 0; b < BAT; ++b) {
+        const int qq = (g % NBP) * BAT + b;
+        const int m = m0 + tile_row(ph, wave * IPP * RPI + qq * RPI + lrow);
         const bool ok = m < M && n < N;
         float ssq = 0.f;                              // sum of squares of this lane's stored values
         if constexpr (RES) {
@@ -691,30 +716,35 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
         if constexpr (SUMSQ) {
           // partial sum of squares over 32 lanes (32 * VEC columns, one float
           // per 512 bytes of output row): the two 16-lane row sums of each
-          // half wave, even row first, parked in lane q * RPI + half (bf16:
-          // the half's tile row; fp32: row q, half = part) of ssacc, which
-          // is stored once per pass
+          // half wave, even row first, parked in lane ql + half (bf16: the
+          // wave's rows ql, ql + 1; fp32: row ql, half = part) of ssacc,
+          // which is stored once per pass
           if (!SCAT || ea.row_sumsq != nullptr) {
             const int ri = __builtin_bit_cast(int, row16_sum(ssq));
             const float sa = __builtin_bit_cast(float, __builtin_amdgcn_readlane(ri, 0)) +
                              __builtin_bit_cast(float, __builtin_amdgcn_readlane(ri, 16));
             const float sb = __builtin_bit_cast(float, __builtin_amdgcn_readlane(ri, 32)) +
                              __builtin_bit_cast(float, __builtin_amdgcn_readlane(ri, 48));
-            const int q = ib * BATCH + b;
+            const int ql = (ph * IPP + qq) * RPI;
             constexpr int HB = RPI == 2 ? 1 : 32;       // lane offset of the upper half's value
-            ssacc = lane == q * RPI ? sa : ssacc;
-            ssacc = lane == q * RPI + HB ? sb : ssacc;
+            ssacc = lane == ql ? sa : ssacc;
+            ssacc = lane == ql + HB ? sb : ssacc;
           }
         }
+      }
+      // the next phase's rows: their math runs while this phase's stores drain
+      if ((g + 1) % NBP == 0 && g + 1 < NBT) {
+        stage((g + 1) / NBP);
+        wg_barrier();
       }
     }
     if constexpr (SUMSQ) {
       // one store of the pass's row sums per wave: bf16, lane l < WROWS
-      // holds wave row l (part n0 / 256); fp32, lane l with l % 32 < WROWS
-      // holds wave row l % 32, part n0 / 128 + l / 32
+      // holds the wave's row l (part n0 / 256); fp32, lane l with l % 32 <
+      // WROWS holds the wave's row l % 32, part n0 / 128 + l / 32
       if (!SCAT || ea.row_sumsq != nullptr) {
         const int rw = RPI == 2 ? lane : (lane & 31);
-        const int m = m0 + prow0 + wave * WROWS + rw;
+        const int m = m0 + wave_row(rw < WROWS ? rw : 0);
         const int pcol = n0 + (RPI == 2 ? 0 : (lane >> 5) * 32 * VEC);   // first column of the part
         const int orw = MAPPED ? lmap : m;                                 // lmap: row lane % WROWS (= rw here)
         if (rw < WROWS && m < M && pcol < N) ea.row_sumsq[(int64_t)orw * ea.nparts + pcol / (32 * VEC)] = ssacc;
