@@ -86,8 +86,16 @@ __global__ __launch_bounds__(256) void wsum_partial_kernel(const TP* __restrict_
         for (int u = 0; u < U; ++u) {
           const int f = f0 + u * 64 + lane;
           if (f < wq) {
-            load4<TP>(pr + 4 * f, p[u]);
-            t[u] = *reinterpret_cast<const f32x4*>(tr + 4 * f);
+            // non-temporal: both fields are read once (580 MB at config 5,
+            // twice the last-level cache): 108 -> 95 us per call
+            if constexpr (sizeof(TP) == 4) {
+              const f32x4 pv = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(pr + 4 * f));
+              p[u][0] = pv[0]; p[u][1] = pv[1]; p[u][2] = pv[2]; p[u][3] = pv[3];
+            } else {
+              const bf16x4 pv = __builtin_nontemporal_load(reinterpret_cast<const bf16x4*>(pr + 4 * f));
+              p[u][0] = (float)pv[0]; p[u][1] = (float)pv[1]; p[u][2] = (float)pv[2]; p[u][3] = (float)pv[3];
+            }
+            t[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(tr + 4 * f));
           }
         }
 #pragma unroll
