@@ -17,7 +17,7 @@ from .swin_helpers import (Block, SwinTransformerBlock, WindowAttention, WindowM
                            roll_forward_reverseroll_backward, window_partition, window_reverse)
 from .swin import Conv2DLayer, PatchEmbedLayer, SwinTransformer, TimeStepper, get_model
 from .inference import Rollout
-from . import checkpoint, ops, torch_ops   # torch_ops registers torch.ops.nsw.*
+from . import checkpoint, ops, profiler_utils, torch_ops   # torch_ops registers torch.ops.nsw.*
 
 __all__ = [
     "Block", "SwinTransformerBlock", "WindowMultiHeadAttention", "WindowAttention", "MLP",
@@ -25,4 +25,5 @@ __all__ = [
     "roll_forward_reverseroll_backward", "WeightedRMSE", "WeightedACC", "weighted_rmse_acc",
     "build_spherical_area_weights", "get_spatial_coords", "create_dummy_metadata", "checkpoint", "ops",
     "SwinTransformer", "PatchEmbedLayer", "Conv2DLayer", "TimeStepper", "get_model", "Rollout", "torch_ops",
+    "profiler_utils",
 ]

@@ -14,6 +14,7 @@ from torch import nn
 
 from . import _lib, torch_ops
 from .layer_helpers import BiasLayer, LinearLayer
+from .profiler_utils import profile
 
 
 class MLP(nn.Module):
@@ -46,6 +47,7 @@ class MLP(nn.Module):
     def gelu_epilogue(self) -> int:
         return _lib.NSW_EPI_BIAS_GELU_TANH if self.gelu_tanh else _lib.NSW_EPI_BIAS_GELU
 
+    @profile("mlp")
     def forward(self, x, residual=None):
         """``residual`` (same shape as the output) is added in fc2's epilogue;
         the reference adds the block's skip right after the MLP

@@ -28,6 +28,7 @@ from torch import nn
 
 from . import ops, torch_ops
 from .layer_helpers import LinearLayer, trunc_normal_
+from .profiler_utils import profile
 from .swin_helpers import Block as BlockDefault
 
 _EMBED_META = {"sharded": [], "shared": ["tp-sp1-sp2"], "reduce": ["sp1-sp2"]}
@@ -315,6 +316,7 @@ class SwinTransformer(nn.Module):
         pos = pos.to(device=device, dtype=dtype).expand(B, -1, -1, -1, -1)
         return pos.reshape(-1, self.embed_dim).contiguous()
 
+    @profile("embed")
     def prepare_tokens(self, x: torch.Tensor, invariants: Optional[torch.Tensor] = None,
                        frame0: int = 0) -> torch.Tensor:
         """models/swin.py:269-284: [B, T, C, H, W] -> [B, T, h, w, E]."""
@@ -337,6 +339,7 @@ class SwinTransformer(nn.Module):
             self._head_key = key
         return self._head_w
 
+    @profile("head")
     def forward_head(self, x: torch.Tensor) -> torch.Tensor:
         """models/swin.py:286-299: [B, T, h, w, E] -> [B, T, C_out, H, W]: the
         head GEMM with the reshape + einsum layout in its write-out."""
@@ -365,6 +368,7 @@ class SwinTransformer(nn.Module):
         return out
 
     # -------------------------------------------------------------- forward --
+    @profile("forward")
     def forward(self, x: torch.Tensor, invariants: Optional[torch.Tensor] = None, frame0: int = 0,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """models/swin.py:301-323: [B, T, C_in, H, W] -> [B, 1, C_out, H, W].

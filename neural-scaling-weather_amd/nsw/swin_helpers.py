@@ -23,6 +23,7 @@ import torch.nn as nn
 from . import _lib, ops, torch_ops
 from .layer_helpers import BiasLayer, LinearLayer, NormLayer
 from .mlp import MLP
+from .profiler_utils import profile
 
 
 def window_partition(x: torch.Tensor, window_size: Tuple[int, int]) -> torch.Tensor:
@@ -261,6 +262,7 @@ class Block(nn.Module):
             raise ValueError("temporal dim does not match temporal_context_window_size")
         self.mlp._check_fusable()
 
+    @profile(name="shifted_wmha")
     def _shifted_window_attn(self, x: torch.Tensor) -> torch.Tensor:
         """models/swin_helpers.py:399-433 on an already-normalised x."""
         B, T, H, W, C = x.shape
