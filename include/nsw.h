@@ -384,6 +384,22 @@ int nsw_head_unpatchify(const void* x, const void* w_perm, void* out, int64_t B,
                         int64_t W, int64_t p, int64_t K, int64_t out_bstride, int dtype, int out_dtype,
                         void* stream);
 
+/* SwinTransformer's big skip (use_big_skip_conv, models/swin.py:212-223 and
+ * :310-319): skip_conv = Conv2d(C_in -> C_out, 1x1, no bias) of the input,
+ * added to the head's image, of which the model returns the last frame.
+ * In place on that frame: out[b*out_bstride + co*H*W + q] +=
+ * sum_ci w[co*C_in + ci] * xin[b, ci, q], xin = frame (T - 1 + frame0) mod T
+ * of x [B, T, C_x, H, W] (x_dtype) followed by the C_inv invariant planes
+ * inv [C_inv, H, W] (same dtype), C_in = C_x + C_inv.  w is float32
+ * [C_out, C_in].  The input values and the convolution are rounded to
+ * model_dtype (the reference's conv runs on the model-dtype input and
+ * returns that dtype, then the two model-dtype images are added), the sum to
+ * out_dtype.  Requires H*W a multiple of 4, C_out*C_in <= 16384, out_bstride
+ * >= C_out*H*W and a multiple of 4, x / inv / out aligned to 4 elements. */
+int nsw_skip_conv_accumulate(const void* x, const void* inv, const float* w, void* out, int64_t B, int64_t T,
+                             int64_t C_x, int64_t C_inv, int64_t C_out, int64_t H, int64_t W, int64_t frame0,
+                             int64_t out_bstride, int x_dtype, int model_dtype, int out_dtype, void* stream);
+
 /* HBM stream probe.  No counterpart in the reference: a measurement helper
  * for callers that report kernel rates against what the device sustains
  * (bench.py's achievable peaks).  dst == NULL: reads `bytes` from src with

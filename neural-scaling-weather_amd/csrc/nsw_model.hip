@@ -368,6 +368,64 @@ static int rows_per_wg(int budget, int row_bytes) {
 
 }  // namespace nsw
 
+namespace nsw {
+
+// SwinTransformer's big skip (use_big_skip_conv, models/swin.py:212-223,
+// 310-319): a 1x1 convolution without bias from the input channels to the
+// output channels, added to the head's image.  Only the predicted frame is
+// returned (x[:, -1:]), so only the window's last frame is convolved:
+//   out[b, co, q] = R_o(out[b, co, q] + R_m(sum_ci w[co, ci] R_m(xin[b, ci, q])))
+// with xin = x's frame (T - 1 + frame0) mod T of the ring, then the invariant
+// planes; R_m rounds to the model's dtype (the reference convolves the
+// model-dtype input and returns the model dtype, then adds two model-dtype
+// tensors), R_o to out's dtype.  A thread owns 4 consecutive pixels and CPT
+// output channels (blockIdx.y), the weight [C_out, C_in] sits in LDS.
+template <typename TX, typename TO, typename TM, int CPT>
+__global__ __launch_bounds__(256) void skip_conv_kernel(const TX* __restrict__ x, const TX* __restrict__ inv,
+                                                        const float* __restrict__ w, TO* __restrict__ out,
+                                                        int C_x, int C_inv, int C_out, int T, int slot,
+                                                        int64_t HW, int64_t out_bstride) {
+  extern __shared__ float wl[];
+  const int C = C_x + C_inv;
+  for (int i = threadIdx.x; i < C_out * C; i += 256) wl[i] = w[i];
+  __syncthreads();
+  const int b = blockIdx.z;
+  const int co0 = blockIdx.y * CPT;
+  const int64_t q0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (q0 >= HW) return;
+  float acc[CPT][4];
+#pragma unroll
+  for (int j = 0; j < CPT; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[j][e] = 0.f;
+  const TX* xb = x + ((int64_t)b * T + slot) * C_x * HW + q0;
+  for (int ci = 0; ci < C; ++ci) {
+    const TX* src = ci < C_x ? xb + (int64_t)ci * HW : inv + (int64_t)(ci - C_x) * HW + q0;
+    float v[4];
+    load4<TX>(src, v);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = to_f32(from_f32<TM>(v[e]));
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const float wv = co0 + j < C_out ? wl[(co0 + j) * C + ci] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[j][e] = fmaf(wv, v[e], acc[j][e]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) {
+    if (co0 + j >= C_out) break;
+    TO* o = out + (int64_t)b * out_bstride + (int64_t)(co0 + j) * HW + q0;
+    float cur[4], r[4];
+    load4<TO>(o, cur);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = cur[e] + to_f32(from_f32<TM>(acc[j][e]));
+    store4<TO>(o, r);
+  }
+}
+
+}  // namespace nsw
+
 using namespace nsw;
 
 extern "C" int nsw_patch_im2col(const void* x, const void* inv, int64_t B, int64_t T, int64_t C_x,
@@ -500,5 +558,51 @@ extern "C" int nsw_unpatchify(const void* y, void* out, int64_t B, int64_t C_out
   else return set_error(NSW_ERR_INVALID, "%s: unknown dtype pair %d -> %d", what, in_dtype, out_dtype);
 #undef NSW_UNPATCH_P
 #undef NSW_UNPATCH
+  return check_launch(what);
+}
+
+extern "C" int nsw_skip_conv_accumulate(const void* x, const void* inv, const float* w, void* out, int64_t B,
+                                        int64_t T, int64_t C_x, int64_t C_inv, int64_t C_out, int64_t H,
+                                        int64_t W, int64_t frame0, int64_t out_bstride, int x_dtype,
+                                        int model_dtype, int out_dtype, void* stream) {
+  const char* what = "nsw_skip_conv_accumulate";
+  NSW_CHECK_ARG(B > 0 && T > 0 && C_x > 0 && C_inv >= 0 && C_out > 0 && H > 0 && W > 0,
+                "%s: B, T, C_x, C_out, H, W must be positive (C_inv >= 0)", what);
+  NSW_CHECK_ARG(C_inv == 0 || inv != nullptr, "%s: invariant channels without data", what);
+  NSW_CHECK_ARG(x != nullptr && w != nullptr && out != nullptr, "%s: missing pointer", what);
+  NSW_CHECK_ARG(frame0 >= 0 && frame0 < T, "%s: frame0 must lie in [0, T)", what);
+  NSW_CHECK_ARG((C_x + C_inv) * C_out <= 16384, "%s: C_out x C_in = %lld above 16384 (the weight lives in LDS)",
+                what, (long long)((C_x + C_inv) * C_out));
+  const int64_t HW = H * W;
+  NSW_CHECK_ARG(HW % 4 == 0 && HW < (1LL << 31), "%s: H*W=%lld must be a multiple of 4 (below 2^31)", what,
+                (long long)HW);
+  NSW_CHECK_ARG(out_bstride >= C_out * HW, "%s: out_bstride smaller than one sample", what);
+  const size_t xa = 4 * dtype_size(x_dtype), oa = 4 * dtype_size(out_dtype);
+  NSW_CHECK_ARG(((uintptr_t)x % xa) == 0 && (inv == nullptr || ((uintptr_t)inv % xa) == 0) &&
+                    ((uintptr_t)out % oa) == 0 && (out_bstride * (int64_t)dtype_size(out_dtype)) % (int64_t)oa == 0,
+                "%s: x / inv / out must be aligned to 4 elements", what);
+  NSW_CHECK_ARG(B * T * C_x * HW < (1LL << 40) && B * out_bstride < (1LL << 40), "%s: too large", what);
+  NSW_CHECK_ARG(B < 65536, "%s: B=%lld too large", what, (long long)B);
+  constexpr int CPT = 16;
+  const dim3 g((unsigned)((HW / 4 + 255) / 256), (unsigned)((C_out + CPT - 1) / CPT), (unsigned)B), blk(256);
+  const size_t shm = (size_t)(C_x + C_inv) * C_out * sizeof(float);
+  const int slot = (int)((T - 1 + frame0) % T);
+  hipStream_t st = (hipStream_t)stream;
+#define NSW_SKIP(TX, TO, TM)                                                                                 \
+  hipLaunchKernelGGL((skip_conv_kernel<TX, TO, TM, CPT>), g, blk, shm, st, (const TX*)x, (const TX*)inv, w,  \
+                     (TO*)out, (int)C_x, (int)C_inv, (int)C_out, (int)T, slot, HW, out_bstride)
+#define NSW_SKIP_M(TX, TO)                                                                                   \
+  do {                                                                                                       \
+    if (model_dtype == NSW_DTYPE_BF16) NSW_SKIP(TX, TO, bf16);                                               \
+    else if (model_dtype == NSW_DTYPE_F32) NSW_SKIP(TX, TO, float);                                          \
+    else return set_error(NSW_ERR_INVALID, "%s: unknown model dtype %d", what, model_dtype);                 \
+  } while (0)
+  if (x_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_BF16) NSW_SKIP_M(float, bf16);
+  else if (x_dtype == NSW_DTYPE_F32 && out_dtype == NSW_DTYPE_F32) NSW_SKIP_M(float, float);
+  else if (x_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_BF16) NSW_SKIP_M(bf16, bf16);
+  else if (x_dtype == NSW_DTYPE_BF16 && out_dtype == NSW_DTYPE_F32) NSW_SKIP_M(bf16, float);
+  else return set_error(NSW_ERR_INVALID, "%s: unknown dtype pair %d -> %d", what, x_dtype, out_dtype);
+#undef NSW_SKIP_M
+#undef NSW_SKIP
   return check_launch(what);
 }

@@ -100,6 +100,8 @@ SIGNATURES = {
                                 _int, _vp]),
     "nsw_unpatchify": (_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
     "nsw_head_unpatchify": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _int, _vp]),
+    "nsw_skip_conv_accumulate": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        _int, _int, _int, _vp]),
 }
 
 _lib = None

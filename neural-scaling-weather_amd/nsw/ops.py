@@ -624,6 +624,42 @@ def head_unpatchify(x: torch.Tensor, w_perm: torch.Tensor, B: int, C_out: int, H
     return dst
 
 
+def skip_conv_accumulate(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor,
+                         invariants: Optional[torch.Tensor] = None, frame0: int = 0,
+                         model_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """The big skip of SwinTransformer.forward (models/swin.py:310-319) in
+    place: out [B, 1, C_out, H, W] += Conv2d 1x1 (``weight`` [C_out, C_in]
+    or [C_out, C_in, 1, 1], no bias) of x's last frame (ring slot (T - 1 +
+    frame0) mod T of x [B, T, C_x, H, W]) with the invariant planes
+    [C_inv, H, W] appended; values rounded to ``model_dtype`` (weight's
+    dtype by default) as the reference's model-dtype conv and add."""
+    if x.dim() != 5 or out.dim() != 5:
+        raise ValueError("skip_conv_accumulate: x and out must be [B, T, C, H, W] / [B, 1, C_out, H, W]")
+    B, T, C_x, H, W = x.shape
+    C_inv = 0 if invariants is None else invariants.shape[0]
+    w2 = weight.reshape(weight.shape[0], -1)
+    C_out = w2.shape[0]
+    if w2.shape[1] != C_x + C_inv:
+        raise ValueError(f"skip_conv_accumulate: weight has {w2.shape[1]} input channels, x + invariants "
+                         f"{C_x + C_inv}")
+    if tuple(out.shape) != (B, 1, C_out, H, W) or out.stride()[2:] != (H * W, W, 1):
+        raise ValueError(f"skip_conv_accumulate: out must be [{B}, 1, {C_out}, {H}, {W}] with contiguous frames")
+    if invariants is not None and (tuple(invariants.shape) != (C_inv, H, W) or invariants.dtype != x.dtype):
+        raise ValueError("skip_conv_accumulate: invariants must be [C_inv, H, W] in x's dtype")
+    xc = x.contiguous()
+    inv = None if invariants is None else invariants.contiguous()
+    wf = w2.detach().to(torch.float32).contiguous()
+    dev = _dev(xc, wf, inv)
+    if out.device != dev:                      # out may be a strided ring slot (frames contiguous)
+        raise RuntimeError("libnsw op arguments are on different devices")
+    md = model_dtype or weight.dtype
+    check(lib().nsw_skip_conv_accumulate(xc.data_ptr(), _p(inv), wf.data_ptr(), out.data_ptr(), B, T, C_x, C_inv,
+                                         C_out, H, W, int(frame0), out.stride(0), dtype_code(xc),
+                                         _lib.NSW_DTYPE_BF16 if md == torch.bfloat16 else _lib.NSW_DTYPE_F32,
+                                         dtype_code(out), _stream(dev)), "skip_conv_accumulate")
+    return out
+
+
 def weighted_metrics_unnorm(pred: torch.Tensor, target: torch.Tensor, std: torch.Tensor, mean: torch.Tensor,
                             weights: torch.Tensor, clim: Optional[torch.Tensor] = None):
     """Weighted RMSE (and ACC with ``clim``) of pred * std + mean against

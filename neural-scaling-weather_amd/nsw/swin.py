@@ -15,9 +15,10 @@ Forward path on the GPU (models/swin.py:301-323):
                   applies the head to the last frame only, which equals the
                   reference's all-frame head followed by ``x[:, -1:]`` because
                   the head is per token.
-The optional big skip convolution (``use_big_skip_conv=True``, off by
-default and in every configuration of the reference's experiments) is not
-implemented and raises.
+  big skip        with ``use_big_skip_conv=True`` (off by default and in every
+                  configuration of the reference's experiments), the 1x1
+                  convolution of the input's predicted frame added to the
+                  head's image in place (nsw_skip_conv_accumulate).
 """
 from __future__ import annotations
 
@@ -213,8 +214,6 @@ class SwinTransformer(nn.Module):
                  coord_pos_embed=True, domain_metadata=None, use_transformer_engine=True,
                  use_big_skip_conv=False, **kwargs):
         super().__init__()
-        if use_big_skip_conv:
-            raise NotImplementedError("use_big_skip_conv=True is not implemented in libnsw")
         if domain_metadata is None:
             raise ValueError("data loader must provide domain metadata")
         self.num_features = self.embed_dim = embed_dim
@@ -253,6 +252,11 @@ class SwinTransformer(nn.Module):
             for i in range(depth)])
         self.out_size = out_chans * patch_size * patch_size
         self.head = LinearLayer(embed_dim, self.out_size, comm_metadata=dict(_EMBED_META))
+        # modulate the skip with a conv (models/swin.py:211-223): added to
+        # the head's image in forward by nsw_skip_conv_accumulate
+        if use_big_skip_conv:
+            self.skip_conv = Conv2DLayer(in_chans, out_chans, kernel_size=1, bias=False,
+                                         comm_metadata=dict(_EMBED_META))
         self.apply(self._init_weights)
         # chain_blocks: run the blocks loop as one C-ABI call that keeps the
         # residual stream in window order between blocks (each block's fc2
@@ -391,7 +395,11 @@ class SwinTransformer(nn.Module):
         else:
             y = self.prepare_tokens(x, invariants=invariants, frame0=frame0)
             y = self.forward_blocks(y)
-        return self._head_last(y, out=out)
+        res = self._head_last(y, out=out)
+        if self.use_big_skip_conv:
+            # x + skip_conv(x) of models/swin.py:310-317, on the frame returned
+            torch.ops.nsw.skip_conv_accumulate(x, self.skip_conv.conv.weight, res, invariants, int(frame0))
+        return res
 
     def _embed_into_chain(self) -> bool:
         """The embedding writes the chain's window-ordered input when the blocks

@@ -287,6 +287,18 @@ def _(x, w_perm, B, C_out, H, W, p, dtype):
     return x.new_empty((B, 1, C_out, H, W), dtype=dtype if dtype is not None else x.dtype)
 
 
+@torch.library.custom_op("nsw::skip_conv_accumulate", mutates_args=("out",))
+def skip_conv_accumulate(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, invariants: Optional[torch.Tensor],
+                         frame0: int) -> None:
+    """The model's big skip added in place to its predicted frame."""
+    ops.skip_conv_accumulate(x, weight, out, invariants=invariants, frame0=frame0)
+
+
+@skip_conv_accumulate.register_fake
+def _(x, weight, out, invariants, frame0):
+    return None
+
+
 # ---------------------------------------------------------------- metrics ---
 
 @torch.library.custom_op("nsw::weighted_metrics", mutates_args=())

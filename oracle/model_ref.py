@@ -114,8 +114,10 @@ def model_forward(x: torch.Tensor, params: Dict[str, torch.Tensor], *, patch_siz
                   window_size: Tuple[int, int], depth: int, num_heads: int, out_chans: int,
                   coords: Optional[torch.Tensor] = None, eps: Optional[float] = None,
                   gelu: str = "none") -> torch.Tensor:
-    """``SwinTransformer.forward`` (models/swin.py:301-323) without the big
-    skip convolution (``use_big_skip_conv=False``, the default).  ``params``
+    """``SwinTransformer.forward`` (models/swin.py:301-323); with a
+    ``skip_conv.conv.weight`` in ``params`` the big skip convolution
+    (``use_big_skip_conv=True``, :305-319) is applied to every frame of the
+    input and added to the head's image before the last frame is taken.  ``params``
     uses the reference's state-dict names; ``coords`` is [T, H, W, 4] for the
     coordinate embedding, None for a learned ``pos_embed`` parameter.  ``eps``
     is the blocks' RMSNorm eps: nn.RMSNorm(eps=None) takes finfo(dtype).eps
@@ -132,6 +134,10 @@ def model_forward(x: torch.Tensor, params: Dict[str, torch.Tensor], *, patch_siz
         y = swin_ref.block_forward(y, bp, num_heads, window_size, block_shift(i, window_size), eps=eps,
                                    gelu=gelu)
     y = forward_head(y, params["head.weight"], p, out_chans)
+    if "skip_conv.conv.weight" in params:
+        b, t, c, h, w = x.shape
+        skip = F.conv2d(x.reshape(b * t, c, h, w), params["skip_conv.conv.weight"])
+        y = y + skip.view(b, t, out_chans, h, w)
     return y[:, -1:]
 
 

@@ -57,11 +57,13 @@ def activations(shape, seed: int = 2) -> torch.Tensor:
 
 def model_params(in_chans: int, out_chans: int, embed_dim: int, depth: int, num_heads: int,
                  patch_size: int, mlp_ratio: float = 4.0, seed: int = 1, coord_pos_embed: bool = True,
-                 pos_shape=None, random_bias: bool = False, random_norm: bool = False) -> Dict[str, torch.Tensor]:
+                 pos_shape=None, random_bias: bool = False, random_norm: bool = False,
+                 big_skip: bool = False) -> Dict[str, torch.Tensor]:
     """Reference-initialised SwinTransformer parameters (state-dict names of
     models/swin.py:120-209): conv weights trunc_normal(0.02) with zero biases
     (models/swin.py:246-256), the learned ``pos_embed`` trunc_normal(0.02)
-    when ``coord_pos_embed`` is False (``pos_shape`` = [1, T, h, w, E])."""
+    when ``coord_pos_embed`` is False (``pos_shape`` = [1, T, h, w, E]), and
+    with ``big_skip`` the 1x1 skip convolution's weight."""
     g = torch.Generator().manual_seed(seed)
     p = patch_size
     out: Dict[str, torch.Tensor] = {}
@@ -81,6 +83,8 @@ def model_params(in_chans: int, out_chans: int, embed_dim: int, depth: int, num_
                           random_norm=random_norm)
         out.update({f"blocks.{i}.{k}": v for k, v in bp.items()})
     out["head.weight"] = trunc_normal((out_chans * p * p, embed_dim), 0.02, g)
+    if big_skip:   # models/swin.py:212-223: Conv2d 1x1, no bias, trunc_normal(0.02) like every conv
+        out["skip_conv.conv.weight"] = trunc_normal((out_chans, in_chans, 1, 1), 0.02, g)
     return out
 
 

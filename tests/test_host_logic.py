@@ -226,3 +226,27 @@ def test_workspace_cache_keeps_buffers_a_capture_has_seen(monkeypatch):
     gc.collect()
     assert rb() is not None and any(t is rb() for t in ops._ws_retired)
     assert c.numel() >= 400 and ops.workspace(400, dev) is c
+
+
+def test_big_skip_conv_parameters():
+    """use_big_skip_conv=True (models/swin.py:212-223): a bias-free 1x1
+    Conv2DLayer skip_conv [out_chans, in_chans, 1, 1], trunc_normal(0.02)
+    initialised, in the state dict under the reference's key; the oracle's
+    parameter set for the same model loads strictly."""
+    import nsw
+    from oracle import synth
+    C_in, C_out, H, W, p, E, heads, depth = 5, 4, 36, 72, 2, 64, 2, 2
+    meta = {"coords": torch.rand(H, W, 3), "sp_shapes": [[H], [W]], "n_channels": C_out}
+    torch.manual_seed(0)
+    m = nsw.SwinTransformer(temporal_context_window_size=1, window_size=(9, 18), patch_size=p, in_chans=C_in,
+                            out_chans=C_out, embed_dim=E, depth=depth, num_heads=heads, use_big_skip_conv=True,
+                            domain_metadata=meta)
+    w = m.skip_conv.conv.weight
+    assert tuple(w.shape) == (C_out, C_in, 1, 1) and m.skip_conv.conv.bias is None
+    assert w.abs().max() <= 0.04 + 1e-6 and 0.005 < w.std().item() < 0.04
+    prm = synth.model_params(C_in, C_out, E, depth, heads, p, seed=5, big_skip=True)
+    m.load_state_dict(prm, strict=True)
+    assert "skip_conv.conv.weight" in m.state_dict()
+    m2 = nsw.SwinTransformer(temporal_context_window_size=1, window_size=(9, 18), patch_size=p, in_chans=C_in,
+                             out_chans=C_out, embed_dim=E, depth=depth, num_heads=heads, domain_metadata=meta)
+    assert not hasattr(m2, "skip_conv")

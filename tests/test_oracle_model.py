@@ -161,3 +161,24 @@ def test_smooth_field_is_standardised_and_smooth():
     # neighbouring pixels are strongly correlated (white noise would give ~0)
     corr = (f[:, :, 1:] * f[:, :, :-1]).mean()
     assert corr > 0.8
+
+
+def test_big_skip_is_the_last_frames_channel_mix():
+    """models/swin.py:305-319: with a zero head the model returns exactly the
+    1x1 skip convolution of the input's last frame (the skip is per frame and
+    the model keeps x[:, -1:]); brute-force channel sums."""
+    B, T, C_in, C_out, H, W, p, E = 2, 3, 4, 3, 18, 36, 2, 16
+    prm = synth.model_params(C_in, C_out, E, 0, 2, p, seed=5, big_skip=True)
+    prm["head.weight"] = torch.zeros_like(prm["head.weight"])
+    x = synth.activations((B, T, C_in, H, W), seed=6)
+    lat = torch.linspace(90, -90, H + 1)[:-1]
+    lon = torch.linspace(0, 360, W + 1)[:-1]
+    coords = mr.model_coords(mr.spatial_coords(lat, lon), T)
+    got = mr.model_forward(x, prm, patch_size=p, window_size=(9, 18), depth=0, num_heads=2, out_chans=C_out,
+                           coords=coords)
+    w = prm["skip_conv.conv.weight"][:, :, 0, 0].double()
+    want = torch.zeros(B, 1, C_out, H, W, dtype=torch.float64)
+    for o in range(C_out):
+        for c in range(C_in):
+            want[:, 0, o] += w[o, c] * x[:, T - 1, c].double()
+    assert torch.allclose(got.double(), want, atol=1e-6, rtol=1e-5)

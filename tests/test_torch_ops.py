@@ -143,3 +143,18 @@ def test_metric_traces_into_one_graph():
     torch.compile(m, backend=cap, fullgraph=True)(torch.randn(2, 1, 3, 8, 16), torch.randn(2, 1, 3, 8, 16))
     assert len(cap.graphs) == 1
     assert count(targets(cap.graphs[0]), "weighted_metrics") == 1
+
+
+def test_model_with_big_skip_traces_into_one_graph():
+    """use_big_skip_conv: the skip is one in-place op on the head's output."""
+    H, W, C = 72, 144, 5
+    meta_d = {"coords": torch.randn(H, W, 3), "sp_shapes": [[H], [W]], "n_channels": C}
+    model = nsw.SwinTransformer(window_size=(9, 18), patch_size=4, in_chans=C, out_chans=C, embed_dim=128,
+                                depth=2, num_heads=2, use_big_skip_conv=True, domain_metadata=meta_d).eval()
+    cap = Capture()
+    torch._dynamo.reset()
+    torch.compile(model, backend=cap, fullgraph=True)(torch.randn(1, 1, C, H, W))
+    assert len(cap.graphs) == 1
+    t = targets(cap.graphs[0])
+    assert count(t, "skip_conv_accumulate") == 1
+    assert count(t, "head_unpatchify") == 1
