@@ -45,6 +45,12 @@ struct AttnArgs {
   float scale;
   int mask_mode;
   WinGeom g;
+  // set by the host for attn_dma_kernel: scale * log2(e), -100 / scale (both
+  // rounded as the kernels' own float expressions), the byte sizes of qkv
+  // and o (below 2^31 there) and the division by heads
+  float zscale, smask;
+  uint32_t qkv_bytes, obytes;
+  FastDiv dheads;
 };
 
 // Additive mask value for (window, query, key); key/query are tokens of the
@@ -359,20 +365,20 @@ __device__ __forceinline__ void store16_asm(const u32x4& rsrc, uint32_t voff, co
 // ds_read_b64_tr_b16, and stores the block's rows of o (NDB / 2 16-byte
 // stores per lane, issued from inline asm; queries past L go to offset
 // obytes, past the end of o, where they are dropped).
-template <int NKB>
+template <int NKB, bool SHIFTED>
 __device__ __forceinline__ void attn_qblock64(const AttnArgs& a, const char* Ks, const char* Vs, const bf16x8 (&qf)[2],
-                                              int q, int win, int head, bool shifted, const uint64_t* cls,
-                                              const u32x4& ro, uint32_t obytes, int fr, int fg) {
+                                              int q, uint32_t win, int head, const uint64_t* cls,
+                                              const u32x4& ro, int fr, int fg) {
   constexpr int HD = 64;
   constexpr int KP = ((NKB * 16 + 31) / 32) * 32;
   constexpr int NS = HD / 32, NDB = HD / 16, NKS = KP / 32;
-  constexpr float LOG2E = 1.4426950408889634f;
   typedef short i16x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) i16x4 lds_s4;
   const int L = a.L, C = a.C;
   const int qc = q < L ? q : L - 1;
-  const float zscale = a.scale * LOG2E;
-  const float smask = -100.0f / a.scale;
+  const float zscale = a.zscale;
+  const float smask = a.smask;
+  const uint32_t obytes = a.obytes;
   const bf16x8 ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
   // S^T = K Q^T, K fragments KD blocks ahead
   constexpr int KD = NKB < 4 ? NKB : 4;
@@ -400,7 +406,7 @@ __device__ __forceinline__ void attn_qblock64(const AttnArgs& a, const char* Ks,
     __builtin_amdgcn_sched_barrier(0);
   }
   // lane: query fr, keys 16 kb + 4 fg + r
-  if (shifted) {
+  if constexpr (SHIFTED) {
     const int qcls = (int)((cls[qc >> 6] >> (qc & 63)) & 1);
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
@@ -485,13 +491,14 @@ __device__ __forceinline__ void attn_qblock64(const AttnArgs& a, const char* Ks,
 // no transposing LDS writes); each wave's Q fragments are loaded into
 // registers alongside.  Waves take query blocks wave, wave + 4, ...
 template <int NKB>
-__global__ __launch_bounds__(256, 3) void attn_dma_kernel(AttnArgs a, int nitems) {
+__global__ __launch_bounds__(256, 3) void attn_dma_kernel(AttnArgs a) {
   constexpr int HD = 64;
   constexpr int KP = ((NKB * 16 + 31) / 32) * 32;
   constexpr int PART = KP * 128;
   constexpr int RG = KP / 8;
   static_assert((2 * RG) % 4 == 0, "copies split evenly over 4 waves");
   constexpr int NDMA = 2 * RG / 4;
+  static_assert(RG % NDMA == 0, "each wave's copies lie in one of K and V");
   constexpr int QPW = (NKB + 3) / 4;
   constexpr int NS = HD / 32, NCLS = (KP + 63) / 64;
   __shared__ __attribute__((aligned(1024))) char smem[2 * PART];
@@ -502,15 +509,14 @@ __global__ __launch_bounds__(256, 3) void attn_dma_kernel(AttnArgs a, int nitems
   const int fr = lane & 15, fg = lane >> 4;
   const int L = a.L, C = a.C;
   const uint32_t ld = 3u * (uint32_t)C;
-  const int item = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  const int win = item / a.heads, head = item - win * a.heads;
-  const uint32_t qkv_bytes = (uint32_t)((uint64_t)nitems / a.heads * L * ld * 2u);
-  const u32x4 rq = uniform_rsrc(a.qkv, qkv_bytes);
-  const uint32_t obytes = (uint32_t)((uint64_t)nitems / a.heads * L * (uint32_t)C * 2u);
-  const u32x4 ro = uniform_rsrc(a.o, obytes);
+  const uint32_t item = (uint32_t)xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  const uint32_t win = a.dheads.div(item);
+  const int head = (int)(item - win * (uint32_t)a.heads);
+  const u32x4 rq = uniform_rsrc(a.qkv, a.qkv_bytes);
+  const u32x4 ro = uniform_rsrc(a.o, a.obytes);
 
   // Q fragments of this wave's query blocks (rows past L re-read row L - 1)
-  const bf16* base = (const bf16*)a.qkv + (int64_t)win * L * ld + head * HD;
+  const bf16* base = (const bf16*)a.qkv + ((size_t)win * (uint32_t)L * ld + (uint32_t)head * HD);
   bf16x8 qf[QPW][NS];
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
@@ -520,42 +526,74 @@ __global__ __launch_bounds__(256, 3) void attn_dma_kernel(AttnArgs a, int nitems
     for (int s = 0; s < NS; ++s) qf[i][s] = *reinterpret_cast<const bf16x8*>(base + qc * ld + 32 * s + 8 * fg);
   }
   // K rows to [0, PART), V rows to [PART, 2 PART): copy j of this wave is
-  // 8-row group d = wave * NDMA + j
+  // 8-row group d = wave * NDMA + j, all of one part (K for waves 0 and 1).
+  // Lane l copies chunk l % 8 of row 8 rg + l / 8; the row's chunk placement
+  // depends on row % 16 (K) or row % 8 (V), so each lane has two K offsets
+  // (even and odd groups) and one V offset, and a copy adds the group's row
+  // offset, a scalar.
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
-  const uint32_t soff = ((uint32_t)win * (uint32_t)L * ld + (uint32_t)head * HD) * 2u;
+  const uint32_t soff = (win * (uint32_t)L * ld + (uint32_t)head * HD) * 2u;
+  const int part = wave * NDMA / RG;                  // uniform
+  const int rg0 = wave * NDMA - part * RG;
+  const int lrow = lane >> 3;
+  const uint32_t lbase = ((uint32_t)lrow * ld + (uint32_t)(part + 1) * (uint32_t)C) * 2u;
+  const uint32_t gstride = 8u * ld * 2u;              // bytes per 8-row group
+  const uint32_t lds0 = sbase + (uint32_t)(part * PART + rg0 * 1024);
+  if (part == 0) {
+    const uint32_t e0 = lbase + (uint32_t)sw_chunk(lrow, lane & 7) * 16u;
+    const uint32_t e1 = lbase + (uint32_t)sw_chunk(8 + lrow, lane & 7) * 16u;
 #pragma unroll
-  for (int j = 0; j < NDMA; ++j) {
-    const int d = wave * NDMA + j;
-    const int part = d / RG, rg = d - part * RG;
-    const int row = rg * 8 + lane / 8;
-    const int lc = part == 0 ? sw_chunk(row, lane % 8) : v_chunk(row, lane % 8);
-    // V rows past L read from offset qkv_bytes, past the end of qkv: the
-    // range check returns zeros, which land in LDS as the padding rows
-    const uint32_t voff = part == 1 && row >= L
-                              ? qkv_bytes
-                              : ((uint32_t)row * ld + (uint32_t)(part + 1) * (uint32_t)C) * 2u + (uint32_t)lc * 16u;
-    dma16(rq, sbase + (uint32_t)(part * PART + rg * 1024), voff, soff);
+    for (int j = 0; j < NDMA; ++j) {
+      const int rg = rg0 + j;
+      dma16(rq, lds0 + (uint32_t)j * 1024u, ((rg & 1) ? e1 : e0) + (uint32_t)rg * gstride, soff);
+    }
+  } else {
+    const uint32_t e = lbase + (uint32_t)v_chunk(lrow, lane & 7) * 16u;
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) {
+      const int rg = rg0 + j;
+      // V rows past L read from offset qkv_bytes, past the end of qkv: the
+      // range check returns zeros, which land in LDS as the padding rows
+      const uint32_t voff = rg * 8 + lrow < L ? e + (uint32_t)rg * gstride : a.qkv_bytes;
+      dma16(rq, lds0 + (uint32_t)j * 1024u, voff, soff);
+    }
   }
 
-  const bool shifted = window_in_last_band(a, win);
+  // the key-class bit sets of the shift mask (last band of windows only)
+  bool shifted = false;
   uint64_t cls[NCLS];
-  {
-    const int thr = shifted ? (a.g.ws0 - a.g.s0) * a.g.ws1 : 0;
-    const int wa = shifted ? a.g.wa : 1;
+#pragma unroll
+  for (int w = 0; w < NCLS; ++w) cls[w] = 0;
+  if (a.mask_mode == MASK_SHIFT) {
+    const uint32_t wi = win - a.g.dnW.div(win) * (uint32_t)a.g.nW;
+    shifted = (int)a.g.dnwb.div(wi) == a.g.nhb - 1;
+  }
+  if (shifted) {
+    const int thr = (a.g.ws0 - a.g.s0) * a.g.ws1;
 #pragma unroll
     for (int w = 0; w < NCLS; ++w) {
-      const int key = 64 * w + lane;
-      cls[w] = __ballot(shifted && key < L && (key % wa) >= thr);
+      const uint32_t key = 64u * w + (uint32_t)lane;
+      const uint32_t r = key - a.g.dwa.div(key) * (uint32_t)a.g.wa;
+      cls[w] = __ballot(key < (uint32_t)L && (int)r >= thr);
     }
   }
   NSW_WAIT_VMCNT(0);
   wg_barrier();
 
+  if (shifted) {
 #pragma unroll
-  for (int i = 0; i < QPW; ++i) {
-    const int qb = wave + 4 * i;
-    if (qb >= NKB) break;
-    attn_qblock64<NKB>(a, smem, smem + PART, qf[i], qb * 16 + fr, win, head, shifted, cls, ro, obytes, fr, fg);
+    for (int i = 0; i < QPW; ++i) {
+      const int qb = wave + 4 * i;
+      if (qb >= NKB) break;
+      attn_qblock64<NKB, true>(a, smem, smem + PART, qf[i], qb * 16 + fr, win, head, cls, ro, fr, fg);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < QPW; ++i) {
+      const int qb = wave + 4 * i;
+      if (qb >= NKB) break;
+      attn_qblock64<NKB, false>(a, smem, smem + PART, qf[i], qb * 16 + fr, win, head, cls, ro, fr, fg);
+    }
   }
 }
 
@@ -811,12 +849,18 @@ static int launch_mfma(const AttnArgs& a, int64_t grid, hipStream_t st) {
 // offsets of the copies (qkv_bytes, the drop offset of the padding rows, plus
 // the item's offset) must stay below 2^32, and the tensors must be 16-byte
 // aligned.
-static int launch_dma(const AttnArgs& a, int64_t items, hipStream_t st) {
-  const int nkb = (a.L + 15) / 16;
-  const uint64_t qkv_bytes = (uint64_t)items / a.heads * a.L * 3ull * a.C * 2ull;
-  if (nkb != 11 || qkv_bytes >= (1ull << 31) || items >= (1ll << 31) || items % a.heads != 0) return -1;
-  if ((uintptr_t)a.qkv % 16 != 0 || (uintptr_t)a.o % 16 != 0) return -1;
-  hipLaunchKernelGGL((attn_dma_kernel<11>), dim3((unsigned)items), dim3(256), 0, st, a, (int)items);
+static int launch_dma(const AttnArgs& a0, int64_t items, hipStream_t st) {
+  const int nkb = (a0.L + 15) / 16;
+  const uint64_t qkv_bytes = (uint64_t)items / a0.heads * a0.L * 3ull * a0.C * 2ull;
+  if (nkb != 11 || qkv_bytes >= (1ull << 31) || items >= (1ll << 31) || items % a0.heads != 0) return -1;
+  if ((uintptr_t)a0.qkv % 16 != 0 || (uintptr_t)a0.o % 16 != 0) return -1;
+  AttnArgs a = a0;
+  a.zscale = a.scale * 1.4426950408889634f;
+  a.smask = -100.0f / a.scale;
+  a.qkv_bytes = (uint32_t)qkv_bytes;
+  a.obytes = (uint32_t)((uint64_t)items / a.heads * a.L * a.C * 2ull);
+  a.dheads = FastDiv::make((uint32_t)a.heads);
+  hipLaunchKernelGGL((attn_dma_kernel<11>), dim3((unsigned)items), dim3(256), 0, st, a);
   return 0;
 }
 
