@@ -124,6 +124,9 @@ def main():
     ap.add_argument("--gemm-only", action="store_true",
                     help="run only the hipBLASLt comparison leg (the block's four GEMM shapes, this library's "
                          "GEMM against torch.matmul) and print its JSON: the command its counter profiles use")
+    ap.add_argument("--gemm-phases", action="store_true",
+                    help="per-tile phase cycles of the block's GEMMs and of plain GEMMs of the same shapes, "
+                         "from nsw/libnsw_stamps.so (build.py --stamps); prints one JSON line and exits")
     ap.add_argument("--no-block-calls", action="store_true",
                     help="skip the config-3 comparison run with one fused call per block (the forward keeps "
                          "the residual stream in window order between blocks)")
@@ -146,6 +149,9 @@ def main():
 
     if args.copy_calibration:
         copy_calibration()
+    if args.gemm_phases:
+        print(json.dumps({"gemm_phases": gemm_phases(torch.device("cuda:0"), args.config, args.norms)}), flush=True)
+        return
     if args.gemm_only:
         B, T, H, W, C = CONFIGS[args.config][:5]
         M = B * T * H * W
@@ -257,11 +263,13 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def block_kernels(blk, x, y_fused, cfg, norms, steps, warmup):
+def block_kernels(blk, x, y_fused, cfg, norms, steps, warmup, after=None):
     """The block's kernels launched one op at a time (the same kernels as the
     fused call) with HIP events between them on the launch stream: per-kernel
     ms, achieved rate and fraction of the binding spec peak.  Returns
-    (kernels, whether the op-by-op output equals the fused call's)."""
+    (kernels, whether the op-by-op output equals the fused call's).  `after`,
+    if given, is called with each kernel's name right after its launch (the
+    phase-stamp reader; its times are then not meaningful)."""
     import torch
     from nsw import _lib, ops
     B, T, H, W, C, heads, ws, shift, dtype = cfg
@@ -339,9 +347,11 @@ def block_kernels(blk, x, y_fused, cfg, norms, steps, warmup):
             # holds its kernel and not the host's launch latency
             torch.cuda._sleep(SPIN_CYCLES)
             ev[0].record(stream)
-            for i, (_, fn) in enumerate(seq):
+            for i, (n_, fn) in enumerate(seq):
                 fn()
                 ev[i + 1].record(stream)
+                if after is not None:
+                    after(n_)
             torch.cuda.synchronize()
             if it >= warmup:
                 for i, n in enumerate(names):
@@ -372,6 +382,88 @@ def block_kernels(blk, x, y_fused, cfg, norms, steps, warmup):
             kern[n] = {"ms": round(t * 1e3, 4), "bound": "hbm", "achieved": round(ach, 1), "unit": "GB/s",
                        "frac": round(ach / PEAK_HBM_GBS, 4)}
     return kern, same
+
+
+def stamp_phases(stamps, ntile):
+    """Per-tile phase means (cycles of s_memtime) from the GEMM's stamp words
+    (start, first stages landed, main loop done, first epilogue phase staged,
+    end, HW_ID, XCC_ID, workgroup id per tile), and the mean gap between a
+    tile's end and the start of the next tile on the same CU."""
+    import numpy as np
+    t = stamps[: ntile * 8].reshape(ntile, 8).astype(np.int64)
+    hw = t[:, 5]
+    # CU of a workgroup: XCC, shader engine (HW_ID 13-15), array (12), CU (8-11)
+    cu = (t[:, 6] & 0xF) * 1000 + ((hw >> 13) & 7) * 100 + ((hw >> 12) & 1) * 20 + ((hw >> 8) & 15)
+    gaps = []
+    for k in np.unique(cu):
+        idx = np.where(cu == k)[0]
+        o = idx[np.argsort(t[idx, 0])]
+        gaps.extend((t[o[1:], 0] - t[o[:-1], 4]).tolist())
+    mean = lambda a: round(float(np.mean(a)), 0)
+    return {"prologue": mean(t[:, 1] - t[:, 0]), "main_loop": mean(t[:, 2] - t[:, 1]),
+            "first_staging": mean(t[:, 3] - t[:, 2]), "rest_of_epilogue": mean(t[:, 4] - t[:, 3]),
+            "total": mean(t[:, 4] - t[:, 0]), "gap_to_next_tile_on_cu": mean(gaps) if gaps else None,
+            "cus": int(len(np.unique(cu))), "tiles": int(ntile)}
+
+
+def gemm_phases(dev, config, norms):
+    """Per-tile phase cycles (s_memtime) of the block's GEMMs, launched one op
+    at a time as in block_kernels, and of plain GEMMs (no epilogue) of the
+    same shapes, through nsw/libnsw_stamps.so (the library with the phase
+    stamps compiled in).  Means over the tiles of the last of 3 launches of
+    each kernel; MFMA issue per tile and SIMD = 16 cycles per
+    v_mfma_f32_16x16x32_bf16 (bf16)."""
+    import numpy as np
+    import torch
+    import nsw
+    from nsw import _lib, ops
+    path = os.path.join(ROOT, "neural-scaling-weather_amd", "nsw", "libnsw_stamps.so")
+    if not os.path.exists(path):
+        raise SystemExit(f"{path} is not built: python neural-scaling-weather_amd/build.py --stamps")
+    _lib.use(path)
+    B, T, H, W, C, heads, ws, shift, dts, desc = CONFIGS[config]
+    dtype = torch.bfloat16 if dts == "bf16" else torch.float32
+    M = B * T * H * W
+    buf = np.zeros(65536 * 8, dtype=np.uint64)
+
+    def read(ntile):
+        torch.cuda.synchronize()
+        _lib.check(_lib.lib().nsw_gemm_read_stamps(buf.ctypes.data, buf.nbytes), "nsw_gemm_read_stamps")
+        return stamp_phases(buf, ntile)
+
+    def tiles(n):
+        return ((M + 255) // 256) * ((n + 255) // 256)
+
+    def mfma_cycles(k):
+        return 256 * 256 * k // (16 * 16 * (32 if dtype == torch.bfloat16 else 4)) // 4 * 16
+
+    shapes = {"qkv": (3 * C, C), "proj_scatter_sumsq": (C, C), "fc1_rowscale": (4 * C, C), "fc2": (C, 4 * C),
+              "qkv_rowscale": (3 * C, C), "proj_sumsq": (C, C), "fc2_to_tokens": (C, 4 * C),
+              "proj_scatter": (C, C), "fc1": (4 * C, C)}
+    res = {"workload": desc, "clock": "s_memtime cycles (shader clock)", "fused": {}, "plain": {}}
+    torch.manual_seed(1001)
+    blk = nsw.Block(C, heads, (H, W), ws, T, shift_size=shift).to(device=dev, dtype=dtype).eval()
+    blk.fold_norm1 = norms == "window"
+    blk.fold_norm2 = norms != "separate"
+    x = torch.randn(B, T, H, W, C, generator=torch.Generator().manual_seed(1002)).to(device=dev, dtype=dtype)
+
+    def after(name):
+        if name in shapes:
+            n, k = shapes[name]
+            res["fused"][name] = dict(read(tiles(n)), mfma_issue=mfma_cycles(k))
+
+    with torch.inference_mode():
+        y = blk(x)
+        block_kernels(blk, x, y, (B, T, H, W, C, heads, ws, shift, dtype), norms, 1, 2, after=after)
+        g = torch.Generator(device=dev).manual_seed(7)
+        for name, (n, k) in (("qkv", (3 * C, C)), ("proj", (C, C)), ("fc1", (4 * C, C)), ("fc2", (C, 4 * C))):
+            a = torch.randn(M, k, device=dev, generator=g).to(dtype)
+            w = (torch.randn(n, k, device=dev, generator=g) * 0.03).to(dtype)
+            for _ in range(3):
+                ops.linear(a, w)
+            res["plain"][name] = dict(read(tiles(n)), mfma_issue=mfma_cycles(k))
+            del a, w
+    return res
 
 
 CALIB_BYTES = 256 << 20

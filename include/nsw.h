@@ -102,6 +102,16 @@ int nsw_make_attention_mask(float* mask, int64_t H, int64_t W, int64_t ws0, int6
  * no GPU. */
 int nsw_selftest_fastdiv(void);
 
+/* Measurement only (no counterpart in the reference): copies the MFMA GEMM's
+ * per-tile phase stamps of the last launch to host memory, 8 64-bit words
+ * per tile (s_memtime at the tile's start, once its first stages have
+ * landed, after the main loop, after the first epilogue phase is staged,
+ * at its end; HW_ID; XCC_ID; workgroup id), for up to 65536 tiles.  Only a
+ * library built with the stamps compiled in (build.py --stamps ->
+ * nsw/libnsw_stamps.so) records them; the default library returns
+ * NSW_ERR_UNSUPPORTED. */
+int nsw_gemm_read_stamps(void* host, size_t bytes);
+
 /* nn.RMSNorm over the last dim (models/layer_helpers.py:101-119):
  * y = x * rsqrt(mean(x^2) + eps) * w, rows x C. */
 int nsw_rmsnorm(const void* x, const void* w, float eps, void* y, int64_t rows, int64_t C,

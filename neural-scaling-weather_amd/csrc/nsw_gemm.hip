@@ -45,6 +45,25 @@
 
 #include "nsw_gemm_common.h"
 
+// Per-tile phase stamps, compiled in only with -DNSW_GEMM_STAMPS=1 (build.py
+// --stamps, which writes nsw/libnsw_stamps.so; the default library has
+// none): thread 0 of each workgroup reads s_memtime when its tile starts,
+// when the prologue's first stages have landed, after the main loop, after
+// the first epilogue phase is staged and at the end, and stores them with
+// HW_ID, XCC_ID and the workgroup id as 8 words at tile * 8 of
+// nsw_gemm_stamps (the first NSW_STAMP_TILES tiles of each launch; every
+// launch overwrites them).  nsw_gemm_read_stamps copies them to the host.
+#ifndef NSW_GEMM_STAMPS
+#define NSW_GEMM_STAMPS 0
+#endif
+#if NSW_GEMM_STAMPS
+constexpr int NSW_STAMP_TILES = 65536;
+__device__ uint64_t nsw_gemm_stamps[NSW_STAMP_TILES * 8];
+#define NSW_STAMP(var) (var) = __builtin_amdgcn_s_memtime()
+#else
+#define NSW_STAMP(var) ((void)0)
+#endif
+
 namespace nsw {
 
 
@@ -130,7 +149,8 @@ __device__ __forceinline__ u32x4 lds_frag(const char* stage, int row, int chunk)
 template <typename T, int PRE, int NC>
 __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X, const T* __restrict__ Wt, int M,
                                              int N, int K, int m0, int n0, const EpiArgs& ea,
-                                             f32x4 (&acc)[NB][MB], int wave, int lane, int rev) {
+                                             f32x4 (&acc)[NB][MB], int wave, int lane, int rev,
+                                             uint64_t& t_ready) {
   constexpr int SLOT = 256 * ROWB;        // one operand's stage: 32 KB
   constexpr int NCA = NC > 0 ? NC : 1;
   constexpr int WR = NC * 8;              // stage rows copied by one wave (64)
@@ -192,6 +212,7 @@ __device__ __forceinline__ void mainloop_256(char* smem, const T* __restrict__ X
     NSW_WAIT_VMCNT(0);
   }
   wg_barrier();
+  NSW_STAMP(t_ready);
 
   const int frow = lane & 15, fg = lane >> 4;
   const int wrow = (wave % WGN) * WTN + frow;  // w rows of this wave (A operand)
@@ -374,8 +395,11 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   // the rounds of tiles on an XCD; odd rounds walk k backwards (serpentine:
   // 7-8% less L2 fetch on the K = 1024 GEMMs of config 2, 1-1.5% faster)
   const int rev = ((int)(blockIdx.x >> 3) / 32) & 1;
-  if (wave < 4) mainloop_256<T, PRE, 8>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane, rev);
-  else mainloop_256<T, PRE, 0>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane, rev);
+  uint64_t ts[5] = {0, 0, 0, 0, 0};   // phase stamps (NSW_GEMM_STAMPS builds only)
+  NSW_STAMP(ts[0]);
+  if (wave < 4) mainloop_256<T, PRE, 8>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane, rev, ts[1]);
+  else mainloop_256<T, PRE, 0>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane, rev, ts[1]);
+  NSW_STAMP(ts[2]);
 
   // ---------------------------------------------------------------- epilogue
   // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
@@ -651,6 +675,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
     prefetch(0, 0);
     stage(0);
     wg_barrier();
+    if (pass == 0) NSW_STAMP(ts[3]);
     if constexpr (EPI == EPI_UNPATCH) {
       switch (ea.img_p) {
         case 1: unpatch_copy_out<T, 1>(stg, ea, M, N, m0 + prow0, n0, tid); break;
@@ -752,6 +777,17 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
     }
     if (pass + 1 < S::PASSES) wg_barrier();          // before the next pass overwrites the staging rows
   }
+#if NSW_GEMM_STAMPS
+  NSW_STAMP(ts[4]);
+  if (tid == 0 && tile < NSW_STAMP_TILES) {
+    uint64_t* o = nsw_gemm_stamps + (size_t)tile * 8;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) o[i] = ts[i];
+    o[5] = (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);    // HW_ID
+    o[6] = (uint64_t)__builtin_amdgcn_s_getreg((31 << 11) | 20);   // XCC_ID
+    o[7] = blockIdx.x;
+  }
+#endif
 }
 
 template <typename T, int EPI, int PRE = PRE_NONE>
@@ -935,6 +971,19 @@ int gemm_linear_remap(const void* x, const void* w, const void* bias, const void
 }  // namespace nsw
 
 using namespace nsw;
+
+extern "C" int nsw_gemm_read_stamps(void* host, size_t bytes) {
+#if NSW_GEMM_STAMPS
+  NSW_CHECK_ARG(host != nullptr && bytes <= sizeof(uint64_t) * 8 * NSW_STAMP_TILES,
+                "nsw_gemm_read_stamps: at most %zu bytes", sizeof(uint64_t) * 8 * (size_t)NSW_STAMP_TILES);
+  if (hipMemcpyFromSymbol(host, HIP_SYMBOL(nsw_gemm_stamps), bytes, 0, hipMemcpyDeviceToHost) != hipSuccess)
+    return set_error(NSW_ERR_HIP, "nsw_gemm_read_stamps: hipMemcpyFromSymbol failed");
+  return 0;
+#else
+  (void)host; (void)bytes;
+  return set_error(NSW_ERR_UNSUPPORTED, "nsw_gemm_read_stamps: library built without phase stamps (build.py --stamps)");
+#endif
+}
 
 extern "C" int nsw_linear(const void* x, const void* w, const void* bias, const void* residual, void* y,
                           int64_t M, int64_t N, int64_t K, int epilogue, int dtype, void* stream) {

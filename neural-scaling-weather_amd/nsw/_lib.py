@@ -57,6 +57,7 @@ SIGNATURES = {
                                        _int, _vp]),
     "nsw_make_attention_mask": (_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp]),
     "nsw_selftest_fastdiv": (_int, []),
+    "nsw_gemm_read_stamps": (_int, [_vp, ctypes.c_size_t]),
     "nsw_rmsnorm": (_int, [_vp, _vp, _f32, _vp, _i64, _i64, _int, _vp]),
     "nsw_layernorm": (_int, [_vp, _vp, _vp, _f32, _vp, _i64, _i64, _int, _vp]),
     "nsw_rmsnorm_roll_partition": (_int, [_vp, _vp, _f32, _vp, _i64, _i64, _i64, _i64, _i64,
@@ -112,6 +113,16 @@ class NswError(RuntimeError):
     """A libnsw entry point returned an error code."""
 
 
+def load(path: str) -> ctypes.CDLL:
+    """Open a build of the library at `path` with the signatures above."""
+    h = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(h, name)
+        fn.restype = res
+        fn.argtypes = args
+    return h
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
@@ -121,13 +132,16 @@ def lib() -> ctypes.CDLL:
                     raise NswError(
                         f"{LIB_PATH} is not built; run `python neural-scaling-weather_amd/build.py` "
                         "(the Swin block has no non-HIP implementation)")
-                h = ctypes.CDLL(LIB_PATH)
-                for name, (res, args) in SIGNATURES.items():
-                    fn = getattr(h, name)
-                    fn.restype = res
-                    fn.argtypes = args
-                _lib = h
+                _lib = load(LIB_PATH)
     return _lib
+
+
+def use(path: str) -> None:
+    """Route every op through the build at `path` (a measurement build such
+    as nsw/libnsw_stamps.so) for the rest of the process."""
+    global _lib
+    with _lock:
+        _lib = load(path)
 
 
 def check(rc: int, what: str = "") -> None:
