@@ -175,6 +175,9 @@ __device__ __forceinline__ u32x4 make_rsrc(const void* p, uint32_t bytes) {
 // when they already live in SGPRs: a wave-uniform value computed along paths
 // the divergence analysis cannot prove uniform would otherwise reach the
 // "s" constraints in a VGPR (an assembler error).
+// NT: the non-temporal form (`nt`), for data read exactly once, so that it
+// does not displace reused lines in the caches.
+template <bool NT = false>
 __device__ __forceinline__ void dma16(const u32x4& rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
   const u32x4 r = {(uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[0]),
                    (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[1]),
@@ -182,10 +185,16 @@ __device__ __forceinline__ void dma16(const u32x4& rsrc, uint32_t lds_addr, uint
                    (uint32_t)__builtin_amdgcn_readfirstlane((int)rsrc[3])};
   const uint32_t l = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr);
   const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)soff);
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(l), "v"(voff), "s"(r), "s"(so)
-               : "m0");
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+                 :
+                 : "s"(l), "v"(voff), "s"(r), "s"(so)
+                 : "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(l), "v"(voff), "s"(r), "s"(so)
+                 : "m0");
 }
 
 // Barrier between waves with no fence (a fence would wait for every copy)

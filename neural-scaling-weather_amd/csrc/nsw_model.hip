@@ -191,8 +191,10 @@ __global__ __launch_bounds__(256) void im2col_dma_kernel(const float* __restrict
     const float* plane = c < Cx ? x + ((int64_t)(b * T + ts) * Cx + c) * HW : inv + (int64_t)(c - Cx) * HW;
     int x0 = jg * TG * P + (lane ^ im2col_swz<P, TO>(cl, u)) * 4;
     x0 = x0 + 4 <= W ? x0 : W - 4;
-    dma16(make_rsrc(plane, (uint32_t)(HW * 4)), lds0 + (uint32_t)d * 1024u, (uint32_t)(((i * P + u) * W + x0) * 4),
-          0u);
+    // non-temporal: the image is read once (290 MB at config 3); 82.1 ->
+    // 73.4 us at config 3, bit-identical
+    dma16<true>(make_rsrc(plane, (uint32_t)(HW * 4)), lds0 + (uint32_t)d * 1024u,
+                (uint32_t)(((i * P + u) * W + x0) * 4), 0u);
   }
   NSW_WAIT_VMCNT(0);
   __syncthreads();
