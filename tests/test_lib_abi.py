@@ -134,6 +134,15 @@ def test_fastdiv_selftest(L):
     assert L.nsw_selftest_fastdiv() == 0
 
 
+def test_gemm_stamps_only_in_the_stamps_build(L):
+    """The default library has no phase stamps: the reader refuses (no HIP
+    call is made)."""
+    from nsw import _lib
+    buf = (ctypes.c_uint64 * 8)()
+    assert L.nsw_gemm_read_stamps(ctypes.addressof(buf), ctypes.sizeof(buf)) == _lib.NSW_ERR_UNSUPPORTED
+    assert b"--stamps" in L.nsw_last_error()
+
+
 def test_token_count_limit(L):
     from nsw import _lib
     # the row maps index tokens in 32 bits: 2^31 tokens and more are refused
