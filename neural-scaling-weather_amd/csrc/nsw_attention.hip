@@ -465,12 +465,12 @@ __device__ __forceinline__ void attn_qblock64(const AttnArgs& a, const char* Ks,
     for (int db = 0; db < NDB; ++db) O[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[ks & 1][db], pf, O[db], 0, 0, 0);
     Z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf, Z, 0, 0, 0);
   }
-  // 16-byte stores after pairing head-dim blocks (as attn_mfma_kernel);
+  // 16-byte pieces after pairing head-dim blocks (as attn_mfma_kernel);
   // queries past L (and whole padding blocks) go to an offset past the
   // end of o, where the store is dropped
   const float inv = __builtin_amdgcn_rcpf(Z[0]);
-  const uint32_t obase = (((uint32_t)win * (uint32_t)L + (uint32_t)q) * (uint32_t)C +
-                          (uint32_t)(head * HD + 8 * (fg >> 1) + 16 * (fg & 1))) * 2u;
+  static_assert(NDB == 4, "two 64-byte halves per row");
+  f32x4 ch[2];
 #pragma unroll
   for (int j = 0; j < NDB / 2; ++j) {
     const bf16x4 e = {(bf16)(O[2 * j][0] * inv), (bf16)(O[2 * j][1] * inv), (bf16)(O[2 * j][2] * inv),
@@ -481,8 +481,29 @@ __device__ __forceinline__ void attn_qblock64(const AttnArgs& a, const char* Ks,
     float l0 = ev[0], l1 = ev[1], h0 = fv[0], h1 = fv[1];
     permlane16_swap(l0, h0);
     permlane16_swap(l1, h1);
-    store16_asm(ro, q < L ? obase + 64u * j : obytes, f32x4{l0, l1, h0, h1});
+    ch[j] = f32x4{l0, l1, h0, h1};
   }
+  // lanes fr and fr ^ 8 trade halves (DPP row_ror:8 within each 16-lane
+  // row), so that each store instruction writes 8 whole 128-byte rows
+  // (first the block's queries 0-7, then 8-15) instead of 64-byte halves
+  // of 16: bit-identical, 0.7% / 2.3% faster at configs 2 / 4.  Four
+  // separate v_mov_dpp: the vector form of update_dpp was merged into one.
+  const bool lo = fr < 8;
+  const int s0 = __builtin_bit_cast(int, lo ? ch[1][0] : ch[0][0]);
+  const int s1 = __builtin_bit_cast(int, lo ? ch[1][1] : ch[0][1]);
+  const int s2 = __builtin_bit_cast(int, lo ? ch[1][2] : ch[0][2]);
+  const int s3 = __builtin_bit_cast(int, lo ? ch[1][3] : ch[0][3]);
+  const f32x4 recv = {__builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(s0, 0x128, 0xF, 0xF, false)),
+                      __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(s1, 0x128, 0xF, 0xF, false)),
+                      __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(s2, 0x128, 0xF, 0xF, false)),
+                      __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(s3, 0x128, 0xF, 0xF, false))};
+  const int q0 = q - fr;                               // the block's first query
+  const uint32_t cb = (uint32_t)(head * HD + 8 * (fg >> 1) + 16 * (fg & 1)) * 2u + (lo ? 0u : 64u);
+  const int qa = q0 + (fr & 7), qb = q0 + 8 + (fr & 7);
+  const uint32_t oa = (((uint32_t)win * (uint32_t)L + (uint32_t)qa) * (uint32_t)C) * 2u + cb;
+  const uint32_t ob = (((uint32_t)win * (uint32_t)L + (uint32_t)qb) * (uint32_t)C) * 2u + cb;
+  store16_asm(ro, qa < L ? oa : obytes, lo ? ch[0] : recv);
+  store16_asm(ro, qb < L ? ob : obytes, lo ? recv : ch[1]);
 }
 
 // One workgroup per (window, head) item, head dim 64, shift mask from indices
