@@ -363,9 +363,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   // epilogue
   __shared__ __attribute__((aligned(1024))) char smem[Stg<T>::SMEM];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int wm = wave / WGN, wn = wave % WGN;
 
   const int MT = (M + BM - 1) / BM, NT = (N + BN - 1) / BN;
@@ -388,7 +386,6 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   for (int i = 0; i < NB; ++i)
 #pragma unroll
     for (int j = 0; j < MB; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int frow = lane & 15, fg = lane >> 4;
 
   // waves 0-3 copy the operands, waves 4-7 do not (see mainloop_256).  The
   // XCD-local workgroup index (blockIdx / 8) over the XCD's 32 CUs counts
@@ -397,9 +394,21 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(const T* __restrict__ 
   const int rev = ((int)(blockIdx.x >> 3) / 32) & 1;
   uint64_t ts[5] = {0, 0, 0, 0, 0};   // phase stamps (NSW_GEMM_STAMPS builds only)
   NSW_STAMP(ts[0]);
-  if (wave < 4) mainloop_256<T, PRE, 8>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane, rev, ts[1]);
-  else mainloop_256<T, PRE, 0>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane, rev, ts[1]);
+  {
+    const int lane0 = (int)threadIdx.x & 63;
+    if (wave < 4) mainloop_256<T, PRE, 8>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane0, rev, ts[1]);
+    else mainloop_256<T, PRE, 0>(smem, X, Wt, M, N, K, m0, n0, ea, acc, wave, lane0, rev, ts[1]);
+  }
   NSW_STAMP(ts[2]);
+  // the lane's ids for the epilogue, from the lane counter and the (scalar)
+  // wave id: kept live across the k loop they were spilled to scratch (2-5
+  // VGPRs per instantiation; with this, none spill, bit-identical, time
+  // unchanged).  Inline asm, or the compiler folds the counter back into the
+  // work-item id and keeps that live.
+  int lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  const int tid = wave * 64 + lane;
+  const int frow = lane & 15, fg = lane >> 4;
 
   // ---------------------------------------------------------------- epilogue
   // lane (frow, fg) of block (nb, mb) holds y[m0 + wm*WTM + mb*16 + frow]
