@@ -86,9 +86,12 @@ def test_unpatchify_bit_exact(device, idt, odt, B, Co, H, W, p):
     import nsw
     h, w = H // p, W // p
     N = p * p * Co
-    if N % (8 if idt == torch.bfloat16 else 4):
-        pytest.skip("row width not a multiple of the vector width")
     y = torch.randn(B * h * w, N, generator=torch.Generator().manual_seed(Co)).to(idt)
+    if N % (8 if idt == torch.bfloat16 else 4):
+        # rows not a whole number of 16-byte vectors: refused, not computed
+        with pytest.raises(ValueError, match="multiple of"):
+            nsw.ops.unpatchify(y.to(device), B, Co, H, W, p, dtype=odt)
+        return
     got = nsw.ops.unpatchify(y.to(device), B, Co, H, W, p, dtype=odt).cpu()
     want = mr.unpatchify_bruteforce(y, B, 1, h, w, p, Co).to(odt)
     assert torch.equal(got, want)
