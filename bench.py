@@ -191,6 +191,20 @@ def main():
 
         kern, same = block_kernels(blk, x, y, (B, T, H, W, C, heads, ws, shift, dtype), args.norms, args.steps,
                                    args.warmup)
+        # The same K fused blocks timed again once the GPU has run this
+        # workload for a while (the op-by-op loop above): from an idle GPU
+        # the first ~25 blocks run slower while the power manager settles
+        # the clocks (2.0 -> 1.5 ms per block at config 2), and the timed
+        # steps above start right after the W warm-up steps.  Reported
+        # beside `value`, which stays the contract's measurement.
+        e2, e3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e2.record(stream)
+        for _ in range(args.steps):
+            y2 = blk(x)
+        e3.record(stream)
+        torch.cuda.synchronize()
+        ms_settled = e2.elapsed_time(e3) / args.steps
+        del y2
     fl = block_flops(B, T, H, W, C, heads, ws)
     peak_f = PEAK_BF16_TFLOPS if dtype == torch.bfloat16 else PEAK_F32_TFLOPS
     names = list(kern)
@@ -222,7 +236,10 @@ def main():
         "config": {"workload": desc, "tokens": M, "block_tflop": round(total_flops / 1e12, 4),
                    "block_tflops_achieved": round(total_flops / (ms_step * 1e-3) / 1e12, 1),
                    "wall_s_timed": round(wall, 4), "ops_path_equals_fused": bool(same),
-                   "block_launches": len(names), "norms": args.norms},
+                   "block_launches": len(names), "norms": args.norms,
+                   "ms_per_step_settled": round(ms_settled, 4),
+                   "settled_note": "the same K fused blocks re-timed after the op-by-op kernel loop; from an idle "
+                                   "GPU the first ~25 blocks run slower while the clocks settle"},
         "roofline": roofline,
         "kernels": kern,
     }
